@@ -1,0 +1,188 @@
+"""aspida_amd -- MI355X (gfx950) implementation of Aspida's quantized-weight GPU path.
+
+The product is the C-ABI library ``libaspidagpu.so`` (HIP kernels + the
+reference shim's symbol surface, declared in ``include/aspidagpu.h``).  This
+module is its host-side Python binding:
+
+* ``LLMGpu`` mirrors the Ada binding ``LLM_GPU`` (src/llm/llm_gpu.ads,
+  llm_gpu.adb:80-185): ``available``, ``matvec``, ``matmul``,
+  ``dense_matvec``, ``free_weight`` over the host-pointer ABI, and
+  ``moe_experts`` mirrors ``LLM_Qwen_GPU.MoE_Experts`` (llm_qwen_gpu.adb).
+* ``dev`` exposes the device-pointer entry points (integers for device
+  addresses and the HIP stream), used with activations already in HBM.
+
+There is no CPU fallback here: if the library is missing or fails to load,
+``load()`` raises.  The Ada host keeps its own CPU fallback, as before.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libaspidagpu.so")
+HEADER = os.path.join(HERE, "..", "include", "aspidagpu.h")
+
+# LLM_Weight.Kind_Code (src/llm/llm_weight.adb:277-292)
+Q4_K, Q6_K, Q5_K, Q3_K, Q2_K, Q8_0 = 0, 1, 2, 3, 4, 5
+KQUANTS = (Q4_K, Q6_K, Q5_K, Q3_K, Q2_K)
+KINDS = KQUANTS + (Q8_0,)
+KIND_NAMES = {Q4_K: "Q4_K", Q6_K: "Q6_K", Q5_K: "Q5_K", Q3_K: "Q3_K", Q2_K: "Q2_K", Q8_0: "Q8_0"}
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q5_K: 176, Q3_K: 110, Q2_K: 84, Q8_0: 272}
+
+_lib = None
+
+
+def weight_bytes(kind, in_dim, out_dim):
+    return out_dim * (in_dim // 256) * BLOCK_BYTES[kind]
+
+
+def load(path=None):
+    """dlopen libaspidagpu.so (RTLD_NOW, as llm_gpu.adb:90) and bind its symbols."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or os.environ.get("ASPIDA_GPU_LIB") or LIB_PATH
+    if not os.path.exists(p):
+        raise RuntimeError(f"libaspidagpu.so not found at {p}: build it with `python -m aspida_amd.build`")
+    L = ctypes.CDLL(p, mode=ctypes.RTLD_GLOBAL)
+    P, I, LG, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float
+    sig = {
+        "aspida_gpu_matvec": (None, [P, LG, I, I, I, P, P]),
+        "aspida_gpu_matmul": (None, [P, LG, I, I, I, I, P, P]),
+        "aspida_gpu_dense_matvec": (None, [P, LG, I, I, P, P]),
+        "aspida_gpu_free_weight": (None, [P]),
+        "aspida_gpu_moe_experts": (None, [P, I, I, I, I, P, P] + [P, LG, I] * 6 + [P, I, P]),
+        "aspida_gpu_last_error": (I, []),
+        "aspida_kq_xsum_dev": (I, [P, I, I, P, P]),
+        "aspida_kq_matvec_dev": (I, [I, P, I, I, P, P, P, P]),
+        "aspida_kq_matmul_dev": (I, [I, P, I, I, I, P, P, P, P]),
+        "aspida_kq_matmul_valu_dev": (I, [I, P, I, I, I, P, P, P, P]),
+        "aspida_kq_dequant_dev": (I, [I, P, I, I, P, P]),
+        "aspida_dense_matvec_dev": (I, [P, I, I, P, P, P]),
+        "aspida_moe_route_dev": (I, [P, I, I, I, I, P, P, P, P, P]),
+        "aspida_moe_work_floats": (LG, [I, I, I, I]),
+        "aspida_moe_experts_dev": (I, [P, I, I, I, I, I, P, P] + [P, LG, I] * 3 + [P, I] * 3 + [P, P, P, P]),
+        "aspida_kq_set_mv_config": (I, [I, I, I]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = L
+    return L
+
+
+def exported_symbols_declared():
+    """Function names declared in include/aspidagpu.h."""
+    import re
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:void|int|long)\s+(aspida_\w+)\s*\(", txt, re.M)))
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class LLMGpu:
+    """Python mirror of the Ada package LLM_GPU over the host-pointer ABI.
+
+    Weights are numpy uint8 buffers (f32 for dense); the library mirrors each
+    into HBM keyed by its address, so keep the array alive and unchanged until
+    ``free_weight``.
+    """
+
+    def __init__(self, path=None):
+        self.lib = load(path)
+
+    def available(self):
+        return True
+
+    def last_error(self):
+        return self.lib.aspida_gpu_last_error()
+
+    def matvec(self, w, kind, in_dim, out_dim, x, wbytes=None):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(out_dim, np.float32)
+        wb = w.nbytes if wbytes is None else wbytes
+        self.lib.aspida_gpu_matvec(_p(w), wb, kind, in_dim, out_dim, _p(x), _p(y))
+        return y
+
+    def matmul(self, w, kind, in_dim, out_dim, x, wbytes=None):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, in_dim)
+        y = np.empty((x.shape[0], out_dim), np.float32)
+        wb = w.nbytes if wbytes is None else wbytes
+        self.lib.aspida_gpu_matmul(_p(w), wb, kind, in_dim, out_dim, x.shape[0], _p(x), _p(y))
+        return y
+
+    def dense_matvec(self, w, x):
+        w = np.ascontiguousarray(w, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(w.shape[0], np.float32)
+        self.lib.aspida_gpu_dense_matvec(_p(w), w.nbytes, w.shape[1], w.shape[0], _p(x), _p(y))
+        return y
+
+    def free_weight(self, w):
+        self.lib.aspida_gpu_free_weight(_p(w))
+
+    def moe_experts(self, x, dim, top_k, intermed, n_exp, top_idx, top_w, gate, up, down, shg, shu, shd,
+                    shared_gate_inp=None):
+        """gate/up/down/shg/shu/shd: (uint8 array, kind) pairs; experts are
+        [n_exp][rows][cols] slabs of bytes / n_exp each."""
+        x = np.ascontiguousarray(x, np.float32)
+        idx = np.ascontiguousarray(top_idx, np.int32)
+        tw = np.ascontiguousarray(top_w, np.float32)
+        y = np.empty(dim, np.float32)
+        args = []
+        for arr, kind in (gate, up, down, shg, shu, shd):
+            args += [_p(arr), arr.nbytes, kind]
+        sgi = None if shared_gate_inp is None else np.ascontiguousarray(shared_gate_inp, np.float32)
+        self.lib.aspida_gpu_moe_experts(_p(x), dim, top_k, intermed, n_exp, _p(idx), _p(tw), *args,
+                                        _p(sgi), 0 if sgi is None else sgi.size, _p(y))
+        return y
+
+
+class DeviceOps:
+    """Device-pointer entry points; pointers and the stream are plain ints."""
+
+    def __init__(self, path=None):
+        self.lib = load(path)
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with code {rc}")
+
+    def xsum(self, x, in_dim, rows, xq, stream=0):
+        self._ok(self.lib.aspida_kq_xsum_dev(x, in_dim, rows, xq, stream), "aspida_kq_xsum_dev")
+
+    def matvec(self, kind, w, in_dim, out_dim, x, xq, y, stream=0):
+        self._ok(self.lib.aspida_kq_matvec_dev(kind, w, in_dim, out_dim, x, xq, y, stream), "aspida_kq_matvec_dev")
+
+    def matmul(self, kind, w, in_dim, out_dim, batch, x, xq, y, stream=0, valu=False):
+        fn = self.lib.aspida_kq_matmul_valu_dev if valu else self.lib.aspida_kq_matmul_dev
+        self._ok(fn(kind, w, in_dim, out_dim, batch, x, xq, y, stream), "aspida_kq_matmul_dev")
+
+    def dequant(self, kind, w, in_dim, out_dim, dst, stream=0):
+        self._ok(self.lib.aspida_kq_dequant_dev(kind, w, in_dim, out_dim, dst, stream), "aspida_kq_dequant_dev")
+
+    def dense(self, w, in_dim, out_dim, x, y, stream=0):
+        self._ok(self.lib.aspida_dense_matvec_dev(w, in_dim, out_dim, x, y, stream), "aspida_dense_matvec_dev")
+
+    def route(self, router_w, n_exp, dim, T, top_k, x, logits, top_idx, top_w, stream=0):
+        self._ok(self.lib.aspida_moe_route_dev(router_w, n_exp, dim, T, top_k, x, logits, top_idx, top_w, stream),
+                 "aspida_moe_route_dev")
+
+    def moe_work_floats(self, T, dim, top_k, intermed):
+        return int(self.lib.aspida_moe_work_floats(T, dim, top_k, intermed))
+
+    def moe_experts(self, x, T, dim, top_k, intermed, n_exp, top_idx, top_w, gate, up, down, shg, shu, shd,
+                    shared_gate_inp, work, y, stream=0):
+        """gate/up/down: (ptr, stride_bytes, kind); shg/shu/shd: (ptr, kind)."""
+        args = [*gate, *up, *down, *shg, *shu, *shd]
+        self._ok(self.lib.aspida_moe_experts_dev(x, T, dim, top_k, intermed, n_exp, top_idx, top_w, *args,
+                                                 shared_gate_inp or 0, work, y, stream),
+                 "aspida_moe_experts_dev")
+
+    def set_mv_config(self, layout, rows_per_wave=4, splits=1):
+        self._ok(self.lib.aspida_kq_set_mv_config(layout, rows_per_wave, splits), "aspida_kq_set_mv_config")

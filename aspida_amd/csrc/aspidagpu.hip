@@ -1,0 +1,464 @@
+// aspidagpu.hip -- the drop-in C ABI (libaspidagpu.so).
+//
+// Exports the symbols Aspida's Ada host resolves with dlopen/dlsym
+// (src/llm/llm_gpu.adb:80-146, src/llm/llm_qwen_gpu.adb:257-266), with the
+// reference shim's signatures (gpu/gpu_matvec.cu:494-553, 925, 1673), plus
+// device-pointer entry points for callers whose activations already live in
+// HBM.  Declarations and contracts: include/aspidagpu.h.
+//
+// Host-ABI calls are synchronous, like the reference's: on return y is fully
+// written.  Unlike the reference they are thread-safe: each calling thread
+// gets its own HIP stream, device scratch and pinned staging buffers, and the
+// VRAM weight cache is guarded by a mutex.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+#include "../../include/aspidagpu.h"
+#include "kq_common.h"
+#include "kq_kernels.h"
+#include "kq_moe.h"
+
+namespace {
+
+// ---- errors -----------------------------------------------------------------
+
+thread_local int t_last_error = 0;
+
+void report(int code, const char* fmt, ...) {
+  t_last_error = code;
+  va_list ap;
+  va_start(ap, fmt);
+  fprintf(stderr, "[aspida_gpu] ");
+  vfprintf(stderr, fmt, ap);
+  fprintf(stderr, "\n");
+  va_end(ap);
+}
+
+int check(hipError_t e, const char* where) {
+  if (e == hipSuccess) return 0;
+  report((int)e, "%s: %s", where, hipGetErrorString(e));
+  return (int)e;
+}
+
+void fill_nan(float* y, long n) {
+  if (!y || n <= 0) return;
+  const float q = std::nanf("");
+  for (long i = 0; i < n; ++i) y[i] = q;
+}
+
+long need_bytes(int kind, int in_dim, int rows) {
+  return (long)rows * (long)(in_dim / 256) * (long)kq::block_bytes(kind);
+}
+
+// ---- VRAM weight cache keyed by host pointer --------------------------------
+
+struct WEnt {
+  void* d;
+  long bytes;
+};
+std::mutex g_wmu;
+std::unordered_map<const void*, WEnt> g_wcache;
+
+// Device mirror of [w, w + bytes).  A cached copy at least that large is
+// reused; a smaller one is replaced.
+void* weight(const void* w, long bytes) {
+  std::lock_guard<std::mutex> lk(g_wmu);
+  auto it = g_wcache.find(w);
+  if (it != g_wcache.end()) {
+    if (it->second.bytes >= bytes) return it->second.d;
+    (void)hipFree(it->second.d);
+    g_wcache.erase(it);
+  }
+  void* d = nullptr;
+  if (check(hipMalloc(&d, (size_t)bytes), "weight upload: hipMalloc")) return nullptr;
+  if (check(hipMemcpy(d, w, (size_t)bytes, hipMemcpyHostToDevice), "weight upload: hipMemcpy")) {
+    (void)hipFree(d);
+    return nullptr;
+  }
+  g_wcache[w] = {d, bytes};
+  return d;
+}
+
+// ---- per-thread execution context -------------------------------------------
+
+template <class T>
+struct DevBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  int ensure(size_t want, const char* what) {
+    if (want <= n) return 0;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+    if (check(hipMalloc(&p, want * sizeof(T)), what)) return -1;
+    n = want;
+    return 0;
+  }
+};
+
+template <class T>
+struct HostBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  int ensure(size_t want, const char* what) {
+    if (want <= n) return 0;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+    if (check(hipHostMalloc((void**)&p, want * sizeof(T), hipHostMallocDefault), what)) return -1;
+    n = want;
+    return 0;
+  }
+};
+
+// Buffers live until the process ends (thread exit does not release them).
+struct Ctx {
+  hipStream_t st = nullptr;
+  DevBuf<float> dx, dy, dq, part, dh;
+  HostBuf<float> hx, hy;
+  DevBuf<int> di;
+  int init() {
+    if (st) return 0;
+    return check(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
+  }
+};
+
+Ctx& ctx() {
+  static thread_local Ctx* c = new Ctx();
+  return *c;
+}
+
+// Launch-shape override for batch-1 matvecs (tuning and tests); layout < 0
+// means "use kq::default_mv_config".
+std::mutex g_cfg_mu;
+int g_cfg_layout = -1, g_cfg_rows = 4, g_cfg_splits = 1;
+
+kq::MvConfig mv_config(int kind, int in_dim, int out_dim) {
+  std::lock_guard<std::mutex> lk(g_cfg_mu);
+  if (g_cfg_layout < 0) return kq::default_mv_config(kind, in_dim, out_dim);
+  kq::MvConfig c;
+  c.layout = (kq::MvLayout)g_cfg_layout;
+  c.rows_per_wave = g_cfg_rows;
+  c.splits = g_cfg_splits;
+  return c;
+}
+
+bool valid_kind(int kind) { return kind >= 0 && kind <= 5; }
+
+int validate_mv(const char* fn, const void* w, long wbytes, int kind, int in_dim, int out_dim, int batch,
+                const float* x, const float* y) {
+  if (!w || !x || !y) { report(-EINVAL, "%s: null pointer argument", fn); return -EINVAL; }
+  if (!valid_kind(kind)) { report(-EINVAL, "%s: unsupported kind %d", fn, kind); return -EINVAL; }
+  if (in_dim <= 0 || out_dim <= 0 || batch <= 0) {
+    report(-EINVAL, "%s: bad shape in=%d out=%d batch=%d", fn, in_dim, out_dim, batch);
+    return -EINVAL;
+  }
+  if (in_dim % 256 != 0) {
+    report(-EINVAL, "%s: in_dim %d is not a multiple of 256", fn, in_dim);
+    return -EINVAL;
+  }
+  if (wbytes < need_bytes(kind, in_dim, out_dim)) {
+    report(-EINVAL, "%s: wbytes %ld < %ld needed for %d x %d kind %d", fn, wbytes,
+           need_bytes(kind, in_dim, out_dim), out_dim, in_dim, kind);
+    return -EINVAL;
+  }
+  return 0;
+}
+
+// x -> device (through pinned staging), per-group sums, then `launch`, then
+// y <- device; synchronous.
+template <class F>
+int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int rows, F&& launch) {
+  if (c.init()) return -1;
+  if (c.dx.ensure((size_t)nx, "hipMalloc x") || c.dy.ensure((size_t)ny, "hipMalloc y") ||
+      c.dq.ensure((size_t)(nx / 16 + 1), "hipMalloc xsum") || c.hx.ensure((size_t)nx, "pinned x") ||
+      c.hy.ensure((size_t)ny, "pinned y"))
+    return -1;
+  std::memcpy(c.hx.p, x, (size_t)nx * sizeof(float));
+  if (check(hipMemcpyAsync(c.dx.p, c.hx.p, (size_t)nx * sizeof(float), hipMemcpyHostToDevice, c.st), "H2D x"))
+    return -1;
+  if (check(kq::launch_xsum(c.dx.p, in_dim, rows, c.dq.p, c.st), "xsum launch")) return -1;
+  if (check(launch(), "kernel launch")) return -1;
+  if (check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)ny * sizeof(float), hipMemcpyDeviceToHost, c.st), "D2H y"))
+    return -1;
+  if (check(hipStreamSynchronize(c.st), "hipStreamSynchronize")) return -1;
+  std::memcpy(y, c.hy.p, (size_t)ny * sizeof(float));
+  return 0;
+}
+
+}  // namespace
+
+// =============================================================================
+// Reference ABI
+// =============================================================================
+
+extern "C" void aspida_gpu_matvec(const void* w, long wbytes, int kind, int in_dim, int out_dim,
+                                  const float* x, float* y) {
+  if (validate_mv("aspida_gpu_matvec", w, wbytes, kind, in_dim, out_dim, 1, x, y)) {
+    fill_nan(y, out_dim);
+    return;
+  }
+  void* dw = weight(w, need_bytes(kind, in_dim, out_dim));
+  Ctx& c = ctx();
+  int rc = dw ? 0 : -1;
+  if (!rc) {
+    const kq::MvConfig cfg = mv_config(kind, in_dim, out_dim);
+    const size_t np = kq::mv_part_floats(cfg, in_dim, out_dim);
+    if (np && c.part.ensure(np, "hipMalloc partials")) rc = -1;
+    if (!rc)
+      rc = run_host(c, x, in_dim, y, out_dim, in_dim, 1, [&]() {
+        return kq::launch_matvec(kind, dw, in_dim, out_dim, c.dx.p, c.dq.p, c.dy.p, c.st, cfg, c.part.p);
+      });
+  }
+  if (rc) fill_nan(y, out_dim);
+}
+
+extern "C" void aspida_gpu_matmul(const void* w, long wbytes, int kind, int in_dim, int out_dim, int batch,
+                                  const float* x, float* y) {
+  if (batch < 1) return;  // nothing to compute (gpu_matvec.cu:538)
+  if (validate_mv("aspida_gpu_matmul", w, wbytes, kind, in_dim, out_dim, batch, x, y)) {
+    fill_nan(y, (long)out_dim * batch);
+    return;
+  }
+  void* dw = weight(w, need_bytes(kind, in_dim, out_dim));
+  Ctx& c = ctx();
+  int rc = dw ? 0 : -1;
+  if (!rc)
+    rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, [&]() {
+      hipError_t e = kq::launch_matmul_mfma(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.st);
+      if (e == hipErrorNotSupported)
+        e = kq::launch_matmul_valu(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dq.p, c.dy.p, c.st);
+      return e;
+    });
+  if (rc) fill_nan(y, (long)out_dim * batch);
+}
+
+extern "C" void aspida_gpu_dense_matvec(const void* w, long wbytes, int in_dim, int out_dim, const float* x,
+                                        float* y) {
+  if (!w || !x || !y || in_dim <= 0 || out_dim <= 0 || wbytes < (long)in_dim * out_dim * 4) {
+    report(-EINVAL, "aspida_gpu_dense_matvec: bad arguments (in=%d out=%d wbytes=%ld)", in_dim, out_dim, wbytes);
+    fill_nan(y, out_dim);
+    return;
+  }
+  void* dw = weight(w, (long)in_dim * out_dim * 4);
+  Ctx& c = ctx();
+  int rc = dw ? 0 : -1;
+  if (!rc) {
+    if (c.init() || c.dx.ensure((size_t)in_dim, "hipMalloc x") || c.dy.ensure((size_t)out_dim, "hipMalloc y") ||
+        c.hx.ensure((size_t)in_dim, "pinned x") || c.hy.ensure((size_t)out_dim, "pinned y"))
+      rc = -1;
+  }
+  if (!rc) {
+    std::memcpy(c.hx.p, x, (size_t)in_dim * 4);
+    rc = check(hipMemcpyAsync(c.dx.p, c.hx.p, (size_t)in_dim * 4, hipMemcpyHostToDevice, c.st), "H2D x");
+    if (!rc) rc = check(kq::launch_dense((const float*)dw, in_dim, out_dim, c.dx.p, c.dy.p, c.st), "dense");
+    if (!rc) rc = check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)out_dim * 4, hipMemcpyDeviceToHost, c.st), "D2H");
+    if (!rc) rc = check(hipStreamSynchronize(c.st), "sync");
+    if (!rc) std::memcpy(y, c.hy.p, (size_t)out_dim * 4);
+  }
+  if (rc) fill_nan(y, out_dim);
+}
+
+extern "C" void aspida_gpu_free_weight(const void* w) {
+  std::lock_guard<std::mutex> lk(g_wmu);
+  auto it = g_wcache.find(w);
+  if (it == g_wcache.end()) return;
+  (void)hipFree(it->second.d);
+  g_wcache.erase(it);
+}
+
+extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int intermed, int n_exp,
+                                       const int* top_idx, const float* top_w, const void* gate_w,
+                                       long gate_bytes, int gate_kind, const void* up_w, long up_bytes,
+                                       int up_kind, const void* down_w, long down_bytes, int down_kind,
+                                       const void* shg_w, long shg_bytes, int shg_kind, const void* shu_w,
+                                       long shu_bytes, int shu_kind, const void* shd_w, long shd_bytes,
+                                       int shd_kind, const float* shared_gate_inp, int gate_inp_len,
+                                       float* y) {
+  const char* fn = "aspida_gpu_moe_experts";
+  if (!x || !y || !top_idx || !top_w || !gate_w || !up_w || !down_w || !shg_w || !shu_w || !shd_w) {
+    report(-EINVAL, "%s: null pointer argument", fn);
+    fill_nan(y, dim);
+    return;
+  }
+  const int kinds[6] = {gate_kind, up_kind, down_kind, shg_kind, shu_kind, shd_kind};
+  bool ok = dim > 0 && intermed > 0 && n_exp > 0 && top_k > 0 && top_k <= n_exp && top_k <= kq::MOE_MAX_TOPK &&
+            dim % 256 == 0 && intermed % 256 == 0;
+  for (int k : kinds) ok = ok && valid_kind(k);
+  if (ok) {
+    const long gb = need_bytes(gate_kind, dim, intermed), ub = need_bytes(up_kind, dim, intermed),
+               db = need_bytes(down_kind, intermed, dim);
+    ok = gate_bytes / n_exp >= gb && up_bytes / n_exp >= ub && down_bytes / n_exp >= db &&
+         shg_bytes >= need_bytes(shg_kind, dim, intermed) && shu_bytes >= need_bytes(shu_kind, dim, intermed) &&
+         shd_bytes >= need_bytes(shd_kind, intermed, dim);
+  }
+  if (ok)
+    for (int k = 0; k < top_k; ++k) ok = ok && top_idx[k] >= 0 && top_idx[k] < n_exp;
+  if (!ok) {
+    report(-EINVAL, "%s: bad arguments (dim=%d intermed=%d n_exp=%d top_k=%d)", fn, dim, intermed, n_exp, top_k);
+    fill_nan(y, dim);
+    return;
+  }
+  kq::MoeWeights mw;
+  // The per-expert stride is bytes / n_exp (gpu_matvec.cu:1702-1703).
+  mw.gate = (const uint8_t*)weight(gate_w, gate_bytes);
+  mw.up = (const uint8_t*)weight(up_w, up_bytes);
+  mw.down = (const uint8_t*)weight(down_w, down_bytes);
+  mw.sh_gate = (const uint8_t*)weight(shg_w, shg_bytes);
+  mw.sh_up = (const uint8_t*)weight(shu_w, shu_bytes);
+  mw.sh_down = (const uint8_t*)weight(shd_w, shd_bytes);
+  mw.gate_stride = gate_bytes / n_exp;
+  mw.up_stride = up_bytes / n_exp;
+  mw.down_stride = down_bytes / n_exp;
+  mw.gate_kind = gate_kind; mw.up_kind = up_kind; mw.down_kind = down_kind;
+  mw.sh_gate_kind = shg_kind; mw.sh_up_kind = shu_kind; mw.sh_down_kind = shd_kind;
+  mw.dim = dim; mw.intermed = intermed; mw.n_exp = n_exp;
+  Ctx& c = ctx();
+  int rc = (mw.gate && mw.up && mw.down && mw.sh_gate && mw.sh_up && mw.sh_down) ? 0 : -1;
+  const bool gated = gate_inp_len > 1 && shared_gate_inp;
+  const float* dsgi = nullptr;
+  if (!rc && gated) {
+    dsgi = (const float*)weight(shared_gate_inp, (long)dim * 4);
+    if (!dsgi) rc = -1;
+  }
+  const size_t scratch = kq::moe_scratch_floats(mw, 1, top_k);
+  if (!rc && (c.init() || c.dx.ensure((size_t)dim, "hipMalloc x") || c.dy.ensure((size_t)dim, "hipMalloc y") ||
+              c.dh.ensure(scratch, "hipMalloc moe scratch") || c.hx.ensure((size_t)dim + 2 * top_k, "pinned x") ||
+              c.hy.ensure((size_t)dim, "pinned y") || c.di.ensure((size_t)top_k, "hipMalloc route")))
+    rc = -1;
+  if (!rc) {
+    // Stage x | top_w | top_idx together in one pinned buffer and one copy.
+    std::memcpy(c.hx.p, x, (size_t)dim * 4);
+    std::memcpy(c.hx.p + dim, top_w, (size_t)top_k * 4);
+    std::memcpy(c.hx.p + dim + top_k, top_idx, (size_t)top_k * 4);
+    rc = check(hipMemcpyAsync(c.dh.p, c.hx.p, ((size_t)dim + 2 * top_k) * 4, hipMemcpyHostToDevice, c.st), "H2D");
+    if (!rc) {
+      const float* dxx = c.dh.p;
+      const float* dtw = c.dh.p + dim;
+      const int* dti = (const int*)(c.dh.p + dim + top_k);
+      float* work = c.dh.p + kq::moe_staging_floats(dim, 1, top_k);
+      rc = check(kq::launch_moe_experts(mw, 1, top_k, dxx, dti, dtw, dsgi, work, c.dy.p, c.st), "moe launch");
+    }
+    if (!rc) rc = check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)dim * 4, hipMemcpyDeviceToHost, c.st), "D2H");
+    if (!rc) rc = check(hipStreamSynchronize(c.st), "sync");
+    if (!rc) std::memcpy(y, c.hy.p, (size_t)dim * 4);
+  }
+  if (rc) fill_nan(y, dim);
+}
+
+extern "C" int aspida_gpu_last_error(void) {
+  const int e = t_last_error;
+  t_last_error = 0;
+  return e;
+}
+
+// =============================================================================
+// Device-pointer entry points (activations already in HBM; asynchronous on
+// `stream`, which may be NULL for the null stream).
+// =============================================================================
+
+extern "C" int aspida_kq_xsum_dev(const float* x, int in_dim, int rows, float* xq, void* stream) {
+  if (!x || !xq || in_dim <= 0 || in_dim % 16 || rows <= 0) return -EINVAL;
+  return check(kq::launch_xsum(x, in_dim, rows, xq, (hipStream_t)stream), "aspida_kq_xsum_dev");
+}
+
+extern "C" int aspida_kq_matvec_dev(int kind, const void* w, int in_dim, int out_dim, const float* x,
+                                    const float* xq, float* y, void* stream) {
+  if (!w || !x || !xq || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
+  const kq::MvConfig cfg = mv_config(kind, in_dim, out_dim);
+  const size_t np = kq::mv_part_floats(cfg, in_dim, out_dim);
+  Ctx& c = ctx();
+  if (np && c.part.ensure(np, "hipMalloc partials")) return -1;
+  return check(kq::launch_matvec(kind, w, in_dim, out_dim, x, xq, y, (hipStream_t)stream, cfg, c.part.p),
+               "aspida_kq_matvec_dev");
+}
+
+extern "C" int aspida_kq_matmul_dev(int kind, const void* w, int in_dim, int out_dim, int batch, const float* x,
+                                    const float* xq, float* y, void* stream) {
+  if (!w || !x || !xq || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || batch <= 0)
+    return -EINVAL;
+  hipError_t e = kq::launch_matmul_mfma(kind, w, in_dim, out_dim, batch, x, y, (hipStream_t)stream);
+  if (e == hipErrorNotSupported)
+    e = kq::launch_matmul_valu(kind, w, in_dim, out_dim, batch, x, xq, y, (hipStream_t)stream);
+  return check(e, "aspida_kq_matmul_dev");
+}
+
+extern "C" int aspida_kq_matmul_valu_dev(int kind, const void* w, int in_dim, int out_dim, int batch,
+                                         const float* x, const float* xq, float* y, void* stream) {
+  if (!w || !x || !xq || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || batch <= 0)
+    return -EINVAL;
+  return check(kq::launch_matmul_valu(kind, w, in_dim, out_dim, batch, x, xq, y, (hipStream_t)stream),
+               "aspida_kq_matmul_valu_dev");
+}
+
+extern "C" int aspida_kq_dequant_dev(int kind, const void* w, int in_dim, int out_dim, float* dst, void* stream) {
+  if (!w || !dst || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
+  return check(kq::launch_dequant(kind, w, in_dim, out_dim, dst, (hipStream_t)stream), "aspida_kq_dequant_dev");
+}
+
+extern "C" int aspida_dense_matvec_dev(const float* w, int in_dim, int out_dim, const float* x, float* y,
+                                       void* stream) {
+  if (!w || !x || !y || in_dim <= 0 || out_dim <= 0) return -EINVAL;
+  return check(kq::launch_dense(w, in_dim, out_dim, x, y, (hipStream_t)stream), "aspida_dense_matvec_dev");
+}
+
+extern "C" int aspida_moe_route_dev(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
+                                    float* logits, int* top_idx, float* top_w, void* stream) {
+  if (!router_w || !x || !logits || !top_idx || !top_w || n_exp <= 0 || dim <= 0 || T <= 0 || top_k <= 0)
+    return -EINVAL;
+  return check(kq::launch_moe_route(router_w, n_exp, dim, T, top_k, x, logits, top_idx, top_w,
+                                    (hipStream_t)stream),
+               "aspida_moe_route_dev");
+}
+
+extern "C" long aspida_moe_work_floats(int T, int dim, int top_k, int intermed) {
+  kq::MoeWeights w;
+  w.dim = dim;
+  w.intermed = intermed;
+  return (long)kq::moe_scratch_floats(w, T, top_k);
+}
+
+extern "C" int aspida_moe_experts_dev(const float* x, int T, int dim, int top_k, int intermed, int n_exp,
+                                      const int* top_idx, const float* top_w, const void* gate_w, long gate_stride,
+                                      int gate_kind, const void* up_w, long up_stride, int up_kind,
+                                      const void* down_w, long down_stride, int down_kind, const void* shg_w,
+                                      int shg_kind, const void* shu_w, int shu_kind, const void* shd_w,
+                                      int shd_kind, const float* shared_gate_inp, float* work, float* y,
+                                      void* stream) {
+  const int kinds[6] = {gate_kind, up_kind, down_kind, shg_kind, shu_kind, shd_kind};
+  bool ok = x && top_idx && top_w && gate_w && up_w && down_w && shg_w && shu_w && shd_w && work && y && T > 0 &&
+            dim > 0 && intermed > 0 && dim % 256 == 0 && intermed % 256 == 0 && top_k > 0 && top_k <= n_exp &&
+            top_k <= kq::MOE_MAX_TOPK;
+  for (int k : kinds) ok = ok && valid_kind(k);
+  if (!ok) return -EINVAL;
+  kq::MoeWeights mw;
+  mw.gate = (const uint8_t*)gate_w; mw.up = (const uint8_t*)up_w; mw.down = (const uint8_t*)down_w;
+  mw.sh_gate = (const uint8_t*)shg_w; mw.sh_up = (const uint8_t*)shu_w; mw.sh_down = (const uint8_t*)shd_w;
+  mw.gate_stride = gate_stride; mw.up_stride = up_stride; mw.down_stride = down_stride;
+  mw.gate_kind = gate_kind; mw.up_kind = up_kind; mw.down_kind = down_kind;
+  mw.sh_gate_kind = shg_kind; mw.sh_up_kind = shu_kind; mw.sh_down_kind = shd_kind;
+  mw.dim = dim; mw.intermed = intermed; mw.n_exp = n_exp;
+  // The staging prefix of the work layout is only used by the host ABI.
+  float* wk = work + kq::moe_staging_floats(dim, T, top_k);
+  return check(kq::launch_moe_experts(mw, T, top_k, x, top_idx, top_w, shared_gate_inp, wk, y,
+                                      (hipStream_t)stream),
+               "aspida_moe_experts_dev");
+}
+
+extern "C" int aspida_kq_set_mv_config(int layout, int rows_per_wave, int splits) {
+  if (layout > 1 || (layout >= 0 && !(rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4 ||
+                                      rows_per_wave == 8)) || splits < 1)
+    return -EINVAL;
+  std::lock_guard<std::mutex> lk(g_cfg_mu);
+  g_cfg_layout = layout;
+  g_cfg_rows = rows_per_wave;
+  g_cfg_splits = splits;
+  return 0;
+}

@@ -1,0 +1,71 @@
+// kq_common.h -- block layouts and device helpers shared by the K-quant kernels.
+//
+// Super-block byte layouts (256 elements each; ggml block_q*_K, restated from
+// src/llm/llm_dequant.adb:110-121, 199-206, 277-289, 329-343, 419-425):
+//   Q4_K 144 B: d f16 | dmin f16 | scales[12] | qs[128]
+//   Q5_K 176 B: d f16 | dmin f16 | scales[12] | qh[32] | qs[128]
+//   Q6_K 210 B: ql[128] | qh[64] | int8 scales[16] | d f16
+//   Q3_K 110 B: hmask[32] | qs[64] | scales[12] | d f16
+//   Q2_K  84 B: scales[16] | qs[64] | d f16 | dmin f16
+//   Q8_0  34 B per 32 elements: d f16 | int8 qs[32]
+// Kind codes are LLM_Weight.Kind_Code's (src/llm/llm_weight.adb:277-292).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kq {
+
+enum Kind : int { Q4_K = 0, Q6_K = 1, Q5_K = 2, Q3_K = 3, Q2_K = 4, Q8_0 = 5 };
+
+__host__ __device__ constexpr int block_bytes(int kind) {
+  return kind == Q4_K ? 144 : kind == Q6_K ? 210 : kind == Q5_K ? 176
+       : kind == Q3_K ? 110 : kind == Q2_K ? 84 : kind == Q8_0 ? 272 : -1;
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Two f16 lanes packed in one dword, reinterpreted.  The K-quant kernels put
+// small unsigned codes q into the mantissa of an f16 whose exponent field is
+// zero: that half is the subnormal q * 2^-24 (or q * 2^(s-24) when the code
+// sits s bits up), exact for q < 1024.  v_fma_mix_f32 then multiplies it by an
+// f32 activation with no separate int->float conversion.
+__device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+
+// acc += lo(p) * xa + hi(p) * xb  (two v_fma_mix_f32).
+__device__ __forceinline__ float fma_pair(uint32_t p, float xa, float xb, float acc) {
+  const half2_t h = as_h2(p);
+  acc = __builtin_fmaf((float)h.x, xa, acc);
+  return __builtin_fmaf((float)h.y, xb, acc);
+}
+
+// IEEE half -> f32 with Aspida's rule that exponent 31 (Inf/NaN) reads as
+// +0.0 (F16_To_F32, src/llm/llm_dequant.adb:46-48).  Subnormal and normal
+// halves convert exactly.
+__device__ __forceinline__ float f16_ada(uint32_t bits16) {
+  const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+  return __builtin_isfinite(f) ? f : 0.0f;
+}
+
+// Unaligned little-endian loads.  Super-blocks of 84/110/210 bytes leave
+// fields only 2- or 4-byte aligned; gfx950 serves dword loads at any such
+// alignment and the compiler emits global_load_dwordx{1,2,4} for these.
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) { uint4 v; __builtin_memcpy(&v, p, 16); return v; }
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) { uint2 v; __builtin_memcpy(&v, p, 8); return v; }
+__device__ __forceinline__ uint32_t ld4(const uint8_t* p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
+__device__ __forceinline__ uint32_t ld2(const uint8_t* p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }
+
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
+  return __builtin_amdgcn_ubfe(v, off, w);
+}
+__device__ __forceinline__ uint32_t rotr(uint32_t v, uint32_t s) {
+  return __builtin_amdgcn_alignbit(v, v, s);
+}
+
+// Sum over a wavefront (64 lanes); every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace kq

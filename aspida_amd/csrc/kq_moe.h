@@ -1,0 +1,46 @@
+// kq_moe.h -- MoE expert FFN on the GPU (host-side launchers, namespace kq).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kq {
+
+constexpr int MOE_MAX_TOPK = 32;
+
+// Device-resident MoE layer weights.  Routed experts are [n_exp][rows][cols]
+// with `*_stride` bytes per expert (gate/up: intermed x dim, down: dim x
+// intermed); the shared expert is one [rows][cols] matrix per projection.
+struct MoeWeights {
+  const uint8_t *gate = nullptr, *up = nullptr, *down = nullptr;
+  const uint8_t *sh_gate = nullptr, *sh_up = nullptr, *sh_down = nullptr;
+  long gate_stride = 0, up_stride = 0, down_stride = 0;
+  int gate_kind = 0, up_kind = 0, down_kind = 1;
+  int sh_gate_kind = 0, sh_up_kind = 0, sh_down_kind = 1;
+  int dim = 0, intermed = 0, n_exp = 0;
+};
+
+// Floats at the front of the work space reserved for staging x | top_w |
+// top_idx (host ABI), rounded up to 16 bytes.
+inline size_t moe_staging_floats(int dim, int T, int top_k) {
+  return ((size_t)T * dim + 2 * (size_t)T * top_k + 3) & ~(size_t)3;
+}
+
+// Floats of work space (staging included) launch_moe_experts needs for T tokens.
+size_t moe_scratch_floats(const MoeWeights& w, int T, int top_k);
+
+// y[t] = sum_k top_w[t][k] * Down_e(silu(Gate_e x_t) * Up_e x_t)  (e = top_idx[t][k],
+// ascending k) + g_t * SharedDown(silu(SharedGate x_t) * SharedUp x_t), where
+// g_t = sigmoid(shared_gate_inp . x_t) when shared_gate_inp is non-null, else 1
+// (LLM_MoE.Forward steps 4-5, src/llm/llm_moe.adb:249-299).  x: [T][dim],
+// top_idx/top_w: [T][top_k] (0-based experts), all device pointers.
+hipError_t launch_moe_experts(const MoeWeights& w, int T, int top_k, const float* x, const int* top_idx,
+                              const float* top_w, const float* shared_gate_inp, float* work, float* y,
+                              hipStream_t s);
+
+// Router: logits[t] = router_w[n_exp][dim] . x[t] (f32), stable softmax,
+// greedy top-k (strict >, lowest index wins ties), renormalised weights
+// (llm_moe.adb:136-197).  Writes top_idx/top_w [T][top_k].
+hipError_t launch_moe_route(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
+                            float* logits, int* top_idx, float* top_w, hipStream_t s);
+
+}  // namespace kq

@@ -1,0 +1,138 @@
+/*
+ * aspidagpu.h -- C ABI of libaspidagpu.so, the MI355X (gfx950) implementation
+ * of Aspida's quantized-weight GPU path.
+ *
+ * Weight kinds are LLM_Weight.Kind_Code's (src/llm/llm_weight.adb:277-292):
+ *   0 = Q4_K (144 B / 256), 1 = Q6_K (210 B), 2 = Q5_K (176 B),
+ *   3 = Q3_K (110 B), 4 = Q2_K (84 B), 5 = Q8_0 (8 x 34 B per 256 elements).
+ * A weight is row-major [out_dim][in_dim / 256 super-blocks] (GGUF ne0 =
+ * in_dim, ne1 = out_dim); activations are contiguous f32, batched ones
+ * [batch][in_dim] / [batch][out_dim].  `long` is 64-bit (LP64), Ada's
+ * Interfaces.C.long.
+ *
+ * Host-pointer entry points (the reference ABI) are synchronous and
+ * thread-safe.  Weights are mirrored into HBM on first use, keyed by host
+ * pointer; the caller must call aspida_gpu_free_weight(w) before freeing or
+ * reusing the host bytes of w, and must not free a weight while another
+ * thread's call is using it.  On invalid arguments or a HIP failure the
+ * output is filled with quiet NaN, a line is printed to stderr and the
+ * calling thread's aspida_gpu_last_error() becomes non-zero.
+ */
+#ifndef ASPIDAGPU_H
+#define ASPIDAGPU_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference ABI (symbols resolved by src/llm/llm_gpu.adb:100-146 and
+ *      src/llm/llm_qwen_gpu.adb:257-266, 340) ------------------------------ */
+
+/* y[out_dim] = W x.  Replaces gpu/gpu_matvec.cu:502-530.  in_dim must be a
+ * multiple of 256 and wbytes >= out_dim * (in_dim / 256) * block bytes.
+ * Kind 4 runs Q2_K and kind 5 Q8_0 (the reference sent every kind >= 4 to
+ * its Q2_K kernel). */
+void aspida_gpu_matvec(const void *w, long wbytes, int kind, int in_dim, int out_dim,
+                       const float *x, float *y);
+
+/* Y[batch][out_dim] = X[batch][in_dim] W^T.  Replaces gpu/gpu_matvec.cu:534-553;
+ * any batch >= 1 is served (the reference clamped batch to 32); batch < 1 is a
+ * no-op as in the reference. */
+void aspida_gpu_matmul(const void *w, long wbytes, int kind, int in_dim, int out_dim, int batch,
+                       const float *x, float *y);
+
+/* y = W x for a dense row-major f32 W [out_dim][in_dim] (e.g. the f32 MoE
+ * router).  Replaces gpu/gpu_matvec.cu:925-935. */
+void aspida_gpu_dense_matvec(const void *w, long wbytes, int in_dim, int out_dim,
+                             const float *x, float *y);
+
+/* Drop the HBM mirror of host weight w; idempotent, a no-op for unknown w.
+ * Replaces gpu/gpu_matvec.cu:494-500. */
+void aspida_gpu_free_weight(const void *w);
+
+/* Routed + shared expert FFN of one MoE layer for one token, routing supplied
+ * by the caller: y = sum_k top_w[k] * Down_e(silu(Gate_e x) * Up_e x)
+ * (e = top_idx[k], 0-based, ascending k) + g * SharedDown(silu(SharedGate x)
+ * * SharedUp x), g = sigmoid(shared_gate_inp . x) when gate_inp_len > 1 and
+ * shared_gate_inp is non-null, else 1.  Routed expert tensors are
+ * [n_exp][rows][cols] with bytes / n_exp per expert.  Replaces
+ * gpu/gpu_matvec.cu:1673-1758; top_k may be up to 32 (the reference silently
+ * truncated it to 8); dim and intermed must be multiples of 256. */
+void aspida_gpu_moe_experts(const float *x, int dim, int top_k, int intermed, int n_exp,
+                            const int *top_idx, const float *top_w,
+                            const void *gate_w, long gate_bytes, int gate_kind,
+                            const void *up_w, long up_bytes, int up_kind,
+                            const void *down_w, long down_bytes, int down_kind,
+                            const void *shg_w, long shg_bytes, int shg_kind,
+                            const void *shu_w, long shu_bytes, int shu_kind,
+                            const void *shd_w, long shd_bytes, int shd_kind,
+                            const float *shared_gate_inp, int gate_inp_len, float *y);
+
+/* Return and clear the calling thread's last error (0 = none).  Same
+ * signature and "return and clear" contract as gpu/gpu_matvec.cu:2348-2352. */
+int aspida_gpu_last_error(void);
+
+/* ---- device-pointer entry points (no counterpart in the reference ABI: for
+ *      callers whose weights and activations already live in HBM, e.g. a
+ *      resident decode chain).  Asynchronous on `stream` (a hipStream_t, NULL =
+ *      null stream); return 0 or a negative errno / positive hipError_t. ---- */
+
+/* xq[r][i] = sum of x[r][16 i .. 16 i + 15], r < rows: the per-group
+ * activation sums the K-quant kernels take (in_dim % 16 == 0). */
+int aspida_kq_xsum_dev(const float *x, int in_dim, int rows, float *xq, void *stream);
+
+/* Device form of aspida_gpu_matvec; xq from aspida_kq_xsum_dev(x). */
+int aspida_kq_matvec_dev(int kind, const void *w, int in_dim, int out_dim, const float *x,
+                         const float *xq, float *y, void *stream);
+
+/* Device form of aspida_gpu_matmul; xq from aspida_kq_xsum_dev(x, .., batch). */
+int aspida_kq_matmul_dev(int kind, const void *w, int in_dim, int out_dim, int batch,
+                         const float *x, const float *xq, float *y, void *stream);
+
+/* Small-batch product forced onto the vector-ALU kernels (the reference
+ * numerics path the MFMA kernels are checked against). */
+int aspida_kq_matmul_valu_dev(int kind, const void *w, int in_dim, int out_dim, int batch,
+                              const float *x, const float *xq, float *y, void *stream);
+
+/* dst[out_dim][in_dim] = dequantized W, bit-identical to the CPU decoders
+ * Decode_Q*K_Block (src/llm/llm_dequant.adb:122-554) and Dequant_Q8_0
+ * (606-630), including their Inf/NaN -> +0.0 reading of f16 scales. */
+int aspida_kq_dequant_dev(int kind, const void *w, int in_dim, int out_dim, float *dst, void *stream);
+
+/* Device form of aspida_gpu_dense_matvec. */
+int aspida_dense_matvec_dev(const float *w, int in_dim, int out_dim, const float *x, float *y,
+                            void *stream);
+
+/* MoE router for T tokens: logits[t][e] = router_w[e][:] . x[t][:] (f32,
+ * [n_exp][dim]), stable softmax, greedy top-k (strict >, lowest index wins
+ * ties), renormalised weights (src/llm/llm_moe.adb:136-197).  Writes
+ * logits[T][n_exp], top_idx[T][top_k] (0-based) and top_w[T][top_k].
+ * n_exp <= 1024, top_k <= 32, dim % 4 == 0. */
+int aspida_moe_route_dev(const float *router_w, int n_exp, int dim, int T, int top_k, const float *x,
+                         float *logits, int *top_idx, float *top_w, void *stream);
+
+/* Floats of `work` aspida_moe_experts_dev needs. */
+long aspida_moe_work_floats(int T, int dim, int top_k, int intermed);
+
+/* Device form of aspida_gpu_moe_experts for T tokens: x [T][dim], top_idx /
+ * top_w [T][top_k], y [T][dim]; routed expert e of a projection starts at
+ * byte e * *_stride of its tensor; shared_gate_inp may be NULL (ungated). */
+int aspida_moe_experts_dev(const float *x, int T, int dim, int top_k, int intermed, int n_exp,
+                           const int *top_idx, const float *top_w,
+                           const void *gate_w, long gate_stride, int gate_kind,
+                           const void *up_w, long up_stride, int up_kind,
+                           const void *down_w, long down_stride, int down_kind,
+                           const void *shg_w, int shg_kind, const void *shu_w, int shu_kind,
+                           const void *shd_w, int shd_kind, const float *shared_gate_inp,
+                           float *work, float *y, void *stream);
+
+/* Launch-shape override for batch-1 matvecs: layout 0 = coalesced (four lanes
+ * per super-block, rows_per_wave in {1, 2, 4, 8}), 1 = one row per lane with
+ * the super-blocks split `splits` ways; layout -1 restores the built-in
+ * choice.  Process-wide; for tuning and tests. */
+int aspida_kq_set_mv_config(int layout, int rows_per_wave, int splits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

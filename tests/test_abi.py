@@ -1,0 +1,100 @@
+"""CPU-only checks of the C-ABI library: it loads, exports every symbol
+include/aspidagpu.h declares (and the five the Ada host resolves), and its
+argument validation rejects bad calls before any GPU work, the way the Ada
+binding would see it: NaN-filled output plus a non-zero aspida_gpu_last_error.
+"""
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+import aspida_amd as aa
+
+# Symbols Aspida's Ada side resolves (src/llm/llm_gpu.adb:100-146,
+# src/llm/llm_qwen_gpu.adb:257-266 and 340).
+ADA_SYMBOLS = ["aspida_gpu_matvec", "aspida_gpu_matmul", "aspida_gpu_dense_matvec",
+               "aspida_gpu_free_weight", "aspida_gpu_moe_experts", "aspida_gpu_last_error"]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return aa.load()
+
+
+def test_header_symbols_exported(lib):
+    declared = aa.exported_symbols_declared()
+    assert set(ADA_SYMBOLS) <= set(declared)
+    out = subprocess.run(["nm", "-D", "--defined-only", aa.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    for s in declared:
+        assert getattr(lib, s) is not None
+
+
+def test_dlopen_like_the_ada_host():
+    """RTLD_NOW dlopen of the library file, then dlsym of each Ada symbol."""
+    h = ctypes.CDLL(aa.LIB_PATH, mode=ctypes.RTLD_LOCAL | 2)
+    for s in ADA_SYMBOLS:
+        assert ctypes.cast(getattr(h, s), ctypes.c_void_p).value
+
+
+def _nan_and_error(g, y):
+    return bool(np.all(np.isnan(y))) and g.last_error() != 0 and g.last_error() == 0
+
+
+def test_matvec_rejects_bad_arguments(lib):
+    g = aa.LLMGpu()
+    g.last_error()
+    x = np.ones(256, np.float32)
+    w = np.zeros(144, np.uint8)
+    assert _nan_and_error(g, g.matvec(w, 0, 300, 1, np.ones(300, np.float32)))   # in % 256 /= 0
+    assert _nan_and_error(g, g.matvec(w, 0, 256, 2, x))                          # wbytes too small
+    assert _nan_and_error(g, g.matvec(w, 9, 256, 1, x))                          # unknown kind
+    assert _nan_and_error(g, g.matvec(w, -1, 256, 1, x))
+    assert _nan_and_error(g, g.matvec(w, 0, 0, 1, x))
+
+
+def test_matmul_batch_zero_is_a_noop(lib):
+    y = np.full(4, 7.0, np.float32)
+    w = np.zeros(144, np.uint8)
+    x = np.ones(256, np.float32)
+    lib.aspida_gpu_matmul(w.ctypes.data, w.nbytes, 0, 256, 1, 0, x.ctypes.data, y.ctypes.data)
+    assert np.all(y == 7.0) and lib.aspida_gpu_last_error() == 0
+
+
+def test_dense_rejects_short_buffer(lib):
+    g = aa.LLMGpu()
+    w = np.zeros((2, 8), np.float32)
+    y = np.empty(3, np.float32)
+    x = np.ones(8, np.float32)
+    lib.aspida_gpu_dense_matvec(w.ctypes.data, w.nbytes, 8, 3, x.ctypes.data, y.ctypes.data)
+    assert np.all(np.isnan(y)) and g.last_error() != 0
+
+
+def test_moe_rejects_bad_routing(lib):
+    g = aa.LLMGpu()
+    dim, inter, n_exp = 256, 256, 2
+    gw = np.zeros(n_exp * inter * 144, np.uint8)
+    dw = np.zeros(n_exp * dim * 210, np.uint8)
+    sg, sd = np.zeros(inter * 144, np.uint8), np.zeros(dim * 210, np.uint8)
+    x = np.ones(dim, np.float32)
+    args = ((gw, 0), (gw, 0), (dw, 1), (sg, 0), (sg, 0), (sd, 1))
+    y = g.moe_experts(x, dim, 2, inter, n_exp, [0, 5], [0.5, 0.5], *args)     # expert id out of range
+    assert np.all(np.isnan(y)) and g.last_error() != 0
+    y = g.moe_experts(x, dim, 3, inter, n_exp, [0, 1, 0], [0.3, 0.3, 0.4], *args)   # top_k > n_exp
+    assert np.all(np.isnan(y)) and g.last_error() != 0
+    y = g.moe_experts(x, 200, 1, inter, n_exp, [0], [1.0], *args)              # dim % 256 /= 0
+    assert np.all(np.isnan(y)) and g.last_error() != 0
+
+
+def test_device_entry_points_reject_bad_arguments(lib):
+    assert lib.aspida_kq_matvec_dev(0, None, 256, 1, None, None, None, None) < 0
+    assert lib.aspida_kq_matvec_dev(7, 1, 256, 1, 1, 1, 1, None) < 0
+    assert lib.aspida_kq_matmul_dev(0, 1, 300, 1, 2, 1, 1, 1, None) < 0
+    assert lib.aspida_kq_dequant_dev(0, 1, 256, 0, 1, None) < 0
+    assert lib.aspida_moe_route_dev(None, 128, 2048, 1, 8, None, None, None, None, None) < 0
+    assert lib.aspida_kq_set_mv_config(0, 3, 1) < 0
+    assert lib.aspida_kq_set_mv_config(2, 4, 1) < 0
+    assert lib.aspida_moe_work_floats(1, 2048, 8, 768) > 9 * 768 * 3
