@@ -63,7 +63,7 @@ def load(path=None):
         "aspida_moe_route_dev": (I, [P, I, I, I, I, P, P, P, P, P]),
         "aspida_moe_work_floats": (LG, [I, I, I, I]),
         "aspida_moe_experts_dev": (I, [P, I, I, I, I, I, P, P] + [P, LG, I] * 3 + [P, I] * 3 + [P, P, P, P]),
-        "aspida_kq_set_mv_config": (I, [I, I, I]),
+        "aspida_kq_set_mv_config": (I, [I, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -184,5 +184,5 @@ class DeviceOps:
                                                  shared_gate_inp or 0, work, y, stream),
                  "aspida_moe_experts_dev")
 
-    def set_mv_config(self, layout, rows_per_wave=4, splits=1):
-        self._ok(self.lib.aspida_kq_set_mv_config(layout, rows_per_wave, splits), "aspida_kq_set_mv_config")
+    def set_mv_config(self, rows_per_wave=0, waves_per_cu=16):
+        self._ok(self.lib.aspida_kq_set_mv_config(rows_per_wave, waves_per_cu), "aspida_kq_set_mv_config")

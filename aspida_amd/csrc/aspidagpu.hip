@@ -121,7 +121,7 @@ struct HostBuf {
 // Buffers live until the process ends (thread exit does not release them).
 struct Ctx {
   hipStream_t st = nullptr;
-  DevBuf<float> dx, dy, dq, part, dh;
+  DevBuf<float> dx, dy, dq, dh;
   HostBuf<float> hx, hy;
   DevBuf<int> di;
   int init() {
@@ -135,18 +135,17 @@ Ctx& ctx() {
   return *c;
 }
 
-// Launch-shape override for batch-1 matvecs (tuning and tests); layout < 0
+// Launch-shape override for batch-1 matvecs (tuning and tests); rows <= 0
 // means "use kq::default_mv_config".
 std::mutex g_cfg_mu;
-int g_cfg_layout = -1, g_cfg_rows = 4, g_cfg_splits = 1;
+int g_cfg_rows = 0, g_cfg_wpc = 16;
 
 kq::MvConfig mv_config(int kind, int in_dim, int out_dim) {
   std::lock_guard<std::mutex> lk(g_cfg_mu);
-  if (g_cfg_layout < 0) return kq::default_mv_config(kind, in_dim, out_dim);
+  if (g_cfg_rows <= 0) return kq::default_mv_config(kind, in_dim, out_dim);
   kq::MvConfig c;
-  c.layout = (kq::MvLayout)g_cfg_layout;
   c.rows_per_wave = g_cfg_rows;
-  c.splits = g_cfg_splits;
+  c.waves_per_cu = g_cfg_wpc;
   return c;
 }
 
@@ -210,12 +209,9 @@ extern "C" void aspida_gpu_matvec(const void* w, long wbytes, int kind, int in_d
   int rc = dw ? 0 : -1;
   if (!rc) {
     const kq::MvConfig cfg = mv_config(kind, in_dim, out_dim);
-    const size_t np = kq::mv_part_floats(cfg, in_dim, out_dim);
-    if (np && c.part.ensure(np, "hipMalloc partials")) rc = -1;
-    if (!rc)
-      rc = run_host(c, x, in_dim, y, out_dim, in_dim, 1, [&]() {
-        return kq::launch_matvec(kind, dw, in_dim, out_dim, c.dx.p, c.dq.p, c.dy.p, c.st, cfg, c.part.p);
-      });
+    rc = run_host(c, x, in_dim, y, out_dim, in_dim, 1, [&]() {
+      return kq::launch_matvec(kind, dw, in_dim, out_dim, c.dx.p, c.dq.p, c.dy.p, c.st, cfg);
+    });
   }
   if (rc) fill_nan(y, out_dim);
 }
@@ -373,10 +369,7 @@ extern "C" int aspida_kq_matvec_dev(int kind, const void* w, int in_dim, int out
                                     const float* xq, float* y, void* stream) {
   if (!w || !x || !xq || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
   const kq::MvConfig cfg = mv_config(kind, in_dim, out_dim);
-  const size_t np = kq::mv_part_floats(cfg, in_dim, out_dim);
-  Ctx& c = ctx();
-  if (np && c.part.ensure(np, "hipMalloc partials")) return -1;
-  return check(kq::launch_matvec(kind, w, in_dim, out_dim, x, xq, y, (hipStream_t)stream, cfg, c.part.p),
+  return check(kq::launch_matvec(kind, w, in_dim, out_dim, x, xq, y, (hipStream_t)stream, cfg),
                "aspida_kq_matvec_dev");
 }
 
@@ -452,13 +445,11 @@ extern "C" int aspida_moe_experts_dev(const float* x, int T, int dim, int top_k,
                "aspida_moe_experts_dev");
 }
 
-extern "C" int aspida_kq_set_mv_config(int layout, int rows_per_wave, int splits) {
-  if (layout > 1 || (layout >= 0 && !(rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4 ||
-                                      rows_per_wave == 8)) || splits < 1)
-    return -EINVAL;
+extern "C" int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu) {
+  if (rows_per_wave > 0 && !(rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4)) return -EINVAL;
+  if (rows_per_wave > 0 && (waves_per_cu < 1 || waves_per_cu > 64)) return -EINVAL;
   std::lock_guard<std::mutex> lk(g_cfg_mu);
-  g_cfg_layout = layout;
   g_cfg_rows = rows_per_wave;
-  g_cfg_splits = splits;
+  g_cfg_wpc = waves_per_cu;
   return 0;
 }

@@ -10,7 +10,9 @@
 //   Q8_0  34 B per 32 elements: d f16 | int8 qs[32]
 // Kind codes are LLM_Weight.Kind_Code's (src/llm/llm_weight.adb:277-292).
 #pragma once
+#ifndef KQ_HOST_EMULATION
 #include <hip/hip_runtime.h>
+#endif
 #include <stdint.h>
 
 namespace kq {
@@ -61,11 +63,13 @@ __device__ __forceinline__ uint32_t rotr(uint32_t v, uint32_t s) {
   return __builtin_amdgcn_alignbit(v, v, s);
 }
 
+#ifndef KQ_HOST_EMULATION
 // Sum over a wavefront (64 lanes); every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+#endif
 
 }  // namespace kq

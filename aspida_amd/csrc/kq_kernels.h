@@ -5,26 +5,20 @@
 
 namespace kq {
 
-enum class MvLayout : int { Coalesced = 0, Lanes = 1 };
-
 struct MvConfig {
-  MvLayout layout = MvLayout::Coalesced;
-  int rows_per_wave = 4;  // Coalesced: 1, 2, 4 or 8
-  int splits = 1;         // Lanes: super-block range split (needs `part`)
+  int rows_per_wave = 2;  // rows per lane group per step: 1, 2 or 4
+  int waves_per_cu = 16;  // resident waves launched per CU (upper bound)
 };
 
 // Launch shape chosen for a batch-1 matvec of this kind and shape.
 MvConfig default_mv_config(int kind, int in_dim, int out_dim);
-
-// Scratch floats launch_matvec needs in `part` for this config (0 if none).
-size_t mv_part_floats(const MvConfig& cfg, int in_dim, int out_dim);
 
 // xq[r][i] = sum of x[r][16i .. 16i+15] for rows r < rows (in_dim % 16 == 0).
 hipError_t launch_xsum(const float* x, int in_dim, int rows, float* xq, hipStream_t s);
 
 // y[out] = W[out][in] x[in] for a quantized W (kinds 0..5); xq from launch_xsum.
 hipError_t launch_matvec(int kind, const void* W, int in_dim, int out_dim, const float* x, const float* xq,
-                         float* y, hipStream_t s, const MvConfig& cfg, float* part);
+                         float* y, hipStream_t s, const MvConfig& cfg);
 
 // Y[b][out] = W X[b] for b < batch, on the vector ALUs; XQ from launch_xsum.
 hipError_t launch_matmul_valu(int kind, const void* W, int in_dim, int out_dim, int batch, const float* X,

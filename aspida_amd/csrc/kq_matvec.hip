@@ -1,19 +1,12 @@
 // kq_matvec.hip -- batch-1 K-quant matvec kernels for gfx950, plus the dense
-// f32 matvec, the bit-exact dequantizer and the small-batch fallback.
+// f32 matvec, the bit-exact dequantizer and the small-batch vector-ALU path.
 //
 // Batch-1 decode is HBM-bound (0.3-0.8 weight bytes per multiply-add), so the
-// kernels stream each weight byte exactly once with 16-byte loads and spend
-// as few VALU instructions per element as possible (v_fma_mix_f32 on f16
-// subnormal codes, see kq_blocks.h).  Two lane layouts are provided:
-//
-//  * kq_mv_coal<K, R>: four lanes per super-block, 16 super-blocks per wave
-//    step, R rows per wave.  Every load instruction reads contiguous bytes;
-//    each lane keeps its 64 activations in registers and reuses them for the
-//    R rows.
-//  * kq_mv_lanes<K>: one row per lane, 64 rows per wave, all lanes at the same
-//    super-block.  The activations are wave-uniform and arrive by scalar
-//    loads; the super-block range is split over blockIdx.y and the partial sums
-//    are added in a fixed order by kq_mv_reduce.
+// kernels stream each weight byte exactly once and spend as few VALU
+// instructions per element as possible (v_fma_mix_f32 on f16 subnormal codes,
+// see kq_blocks.h).  kq_mv_stream keeps every wave resident for the whole
+// launch with its activations in registers, and overlaps the next row
+// block's loads with the current block's arithmetic.
 #include "kq_blocks.h"
 #include "kq_kernels.h"
 
@@ -25,85 +18,104 @@ namespace kq {
 __global__ void xsum16(const float* __restrict__ x, int n16, int rows, float* __restrict__ xq) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n16 * rows) return;
-  const float4* p = (const float4*)(x + (size_t)i * 16);
+  const float* p = x + (size_t)i * 16;
   float s = 0.f;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float4 v = p[k];
-    s += v.x; s += v.y; s += v.z; s += v.w;
-  }
+  for (int k = 0; k < 16; ++k) s += p[k];
   xq[i] = s;
 }
 
+// Row-streaming batch-1 matvec.  A team of nw waves covers one row at a time
+// in chunks: wave w of the team owns super-blocks [w*spl, (w+1)*spl) of every
+// row (spl a power of two <= 16), four lanes per super-block, so a wave
+// covers 64 / (4*spl) rows per step.  Each lane loads the 64 activations of
+// its (super-block, quarter) once and keeps them in registers for the whole
+// launch; the team then walks row blocks blk = team, team + nteams, ... with
+// R rows per lane-group per step, prefetching the next block's weights before
+// computing the current one.  The lanes of a row are reduced with xor
+// shuffles; with nw > 1 the team's partial sums meet in LDS (one team per
+// workgroup then, so the barriers see identical trip counts).
+constexpr int STREAM_MAX_ROWS_STEP = 64;
+
 template <int KIND, int R>
-__global__ __launch_bounds__(256) void kq_mv_coal(const uint8_t* __restrict__ W, size_t row_bytes,
-                                                  int nsb, int out_rows,
-                                                  const float* __restrict__ x,
-                                                  const float* __restrict__ xq,
-                                                  float* __restrict__ y) {
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int row0 = wave * R;
-  if (row0 >= out_rows) return;
-  const int c = lane & 3, slot = lane >> 2;
-  const uint8_t* rp[R];
+__global__ __launch_bounds__(256) void kq_mv_stream(const uint8_t* __restrict__ W, size_t row_bytes,
+                                                    int nsb, int out_rows, const float* __restrict__ x,
+                                                    const float* __restrict__ xq, float* __restrict__ y,
+                                                    int spl_log2, int nw, int nteams) {
+  using B = Block<KIND>;
+  __shared__ float red[16 * STREAM_MAX_ROWS_STEP];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tpw = (int)(blockDim.x >> 6) / nw;
+  const int w = wv % nw;
+  const int team = blockIdx.x * tpw + wv / nw;
+  const int lpr_log2 = spl_log2 + 2;  // lanes per row
+  const int rslot = lane >> lpr_log2;
+  const int within = lane & ((1 << lpr_log2) - 1);
+  const int c = within & 3;
+  const int sb = (w << spl_log2) + (within >> 2);
+  const bool active = sb < nsb;
+  const int sbc = active ? sb : nsb - 1;
+  const int rows_step = (64 >> lpr_log2) * R;
+  const int nblk = (out_rows + rows_step - 1) / rows_step;
+
+  XQuarter xf;
+  B::load_x(x + (size_t)sbc * 256, xq + (size_t)sbc * 16, c, xf);
+  const uint8_t* wcol = W + (size_t)sbc * B::BYTES;
+
+  typename B::W buf0[R], buf1[R];
+  auto load = [&](int blk, typename B::W* dst) {
+    const int r0 = blk * rows_step + rslot * R;
 #pragma unroll
-  for (int r = 0; r < R; ++r) rp[r] = W + (size_t)min(row0 + r, out_rows - 1) * row_bytes;
-  float acc[R];
+    for (int j = 0; j < R; ++j) dst[j] = B::load_w(wcol + (size_t)min(r0 + j, out_rows - 1) * row_bytes, c);
+  };
+  auto compute = [&](int blk, const typename B::W* cur) {
+    float acc[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  for (int sb = slot; sb < nsb; sb += 16) {
-    const float* xs = x + (size_t)sb * 256;
-    const float* qs = xq + (size_t)sb * 16;
+    for (int j = 0; j < R; ++j) acc[j] = active ? B::dot(cur[j], c, xf) : 0.f;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      acc[r] += Block<KIND>::quarter(rp[r] + (size_t)sb * Block<KIND>::BYTES, c, xs, qs);
-  }
+    for (int j = 0; j < R; ++j)
+      for (int o = 1; o < (1 << lpr_log2); o <<= 1) acc[j] += __shfl_xor(acc[j], o, 64);
+    const int r0 = blk * rows_step + rslot * R;
+    if (nw == 1) {
+      if (within == 0) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float v = wave_sum(acc[r]);
-    if (lane == 0 && row0 + r < out_rows) y[row0 + r] = v;
+        for (int j = 0; j < R; ++j)
+          if (r0 + j < out_rows) y[r0 + j] = acc[j];
+      }
+    } else {
+      if (within == 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) red[w * rows_step + rslot * R + j] = acc[j];
+      }
+      __syncthreads();
+      if ((int)threadIdx.x < rows_step) {
+        float s = 0.f;
+        for (int k = 0; k < nw; ++k) s += red[k * rows_step + threadIdx.x];
+        const int r = blk * rows_step + threadIdx.x;
+        if (r < out_rows) y[r] = s;
+      }
+      __syncthreads();
+    }
+  };
+  int blk = team;
+  if (blk < nblk) load(blk, buf0);
+  while (blk < nblk) {
+    const int b1 = blk + nteams;
+    if (b1 < nblk) load(b1, buf1);
+    compute(blk, buf0);
+    if (b1 >= nblk) break;
+    const int b2 = b1 + nteams;
+    if (b2 < nblk) load(b2, buf0);
+    compute(b1, buf1);
+    blk = b2;
   }
 }
 
-template <int KIND>
-__global__ __launch_bounds__(256) void kq_mv_lanes(const uint8_t* __restrict__ W, size_t row_bytes,
-                                                   int nsb, int out_rows, int sb_per_split,
-                                                   const float* __restrict__ x,
-                                                   const float* __restrict__ xq,
-                                                   float* __restrict__ part) {
-  const int lane = threadIdx.x & 63;
-  const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 64 + lane;
-  const int split = blockIdx.y;
-  const uint8_t* rp = W + (size_t)min(row, out_rows - 1) * row_bytes;
-  const int sb0 = split * sb_per_split;
-  const int sb1 = min(nsb, sb0 + sb_per_split);
-  float acc = 0.f;
-  for (int sb = sb0; sb < sb1; ++sb) {
-    const uint8_t* blk = rp + (size_t)sb * Block<KIND>::BYTES;
-    const float* xs = x + (size_t)sb * 256;
-    const float* qs = xq + (size_t)sb * 16;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc += Block<KIND>::quarter(blk, c, xs, qs);
-  }
-  if (row < out_rows) part[(size_t)split * out_rows + row] = acc;
-}
-
-// y[o] = sum over splits s = 0..nsplit-1 (ascending) of part[s][o].
-__global__ void kq_mv_reduce(const float* __restrict__ part, int nsplit, int out_rows,
-                             float* __restrict__ y) {
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= out_rows) return;
-  float s = 0.f;
-  for (int k = 0; k < nsplit; ++k) s += part[(size_t)k * out_rows + o];
-  y[o] = s;
-}
-
-// Small-batch fallback on the vector ALUs: the weights are read once per
-// row-step and applied to every activation row (used when MFMA tiles do not
-// pay, and as the reference path for the MFMA kernels).
+// Small-batch product on the vector ALUs: four lanes per super-block, R rows
+// per wave, the weights re-read (from cache) for each activation row.  The
+// MFMA kernels cover the shapes where this is slow.
 template <int KIND, int R>
-__global__ __launch_bounds__(256) void kq_mm_coal(const uint8_t* __restrict__ W, size_t row_bytes,
+__global__ __launch_bounds__(256) void kq_mm_valu(const uint8_t* __restrict__ W, size_t row_bytes,
                                                   int nsb, int in_dim, int out_rows, int batch,
                                                   const float* __restrict__ X,
                                                   const float* __restrict__ XQ,
@@ -124,8 +136,8 @@ __global__ __launch_bounds__(256) void kq_mm_coal(const uint8_t* __restrict__ W,
       const float* qs = xq + (size_t)sb * 16;
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        acc[r] += Block<KIND>::quarter(W + (size_t)min(row0 + r, out_rows - 1) * row_bytes +
-                                           (size_t)sb * Block<KIND>::BYTES, c, xs, qs);
+        acc[r] += quarter<KIND>(W + (size_t)min(row0 + r, out_rows - 1) * row_bytes +
+                                    (size_t)sb * Block<KIND>::BYTES, c, xs, qs);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -166,8 +178,6 @@ __global__ __launch_bounds__(256) void dense_mv(const float* __restrict__ W, int
 // ---- bit-exact dequantization (test export).  Element P of a super-block is
 // computed with the CPU decoder's own operation order, one rounding, so the
 // f32 bits equal Decode_Q*K_Block's (llm_dequant.adb:122-554).
-__device__ __forceinline__ uint32_t byte_at(const uint8_t* p, int i) { return p[i]; }
-
 template <int KIND>
 __device__ float dequant_elem(const uint8_t* b, int P);
 
@@ -241,54 +251,70 @@ __global__ void kq_dequant(const uint8_t* __restrict__ W, size_t row_bytes, int 
 
 // ---- launchers --------------------------------------------------------------
 
+static int num_cus() {
+  static int n = [] {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    return cus;
+  }();
+  return n;
+}
+
+// Chunk of super-blocks per wave (a power of two <= 16) and waves per team
+// for rows of nsb super-blocks: the chunk that leaves the fewest lanes idle,
+// the larger one on ties, with at most 16 waves per team.
+void stream_shape(int nsb, int& spl_log2, int& nw) {
+  double best = -1.0;
+  spl_log2 = 0;
+  nw = nsb;
+  for (int l = 4; l >= 0; --l) {
+    const int spl = 1 << l;
+    const int n = (nsb + spl - 1) / spl;
+    if (n > 16) continue;
+    const double eff = (double)nsb / (double)(n * spl);
+    if (eff > best + 1e-9) { best = eff; spl_log2 = l; nw = n; }
+  }
+}
+
 MvConfig default_mv_config(int kind, int in_dim, int out_dim) {
   (void)kind;
   (void)in_dim;
+  (void)out_dim;
   MvConfig c;
-  c.layout = MvLayout::Coalesced;
-  // Enough waves to cover 256 CUs several times over, with the largest row
-  // reuse that allows it.
-  c.rows_per_wave = out_dim >= 8192 ? 4 : 2;
-  c.splits = 1;
+  c.rows_per_wave = 2;
+  c.waves_per_cu = 16;
   return c;
-}
-
-size_t mv_part_floats(const MvConfig& cfg, int in_dim, int out_dim) {
-  if (cfg.layout != MvLayout::Lanes || cfg.splits <= 1) return 0;
-  const int nsb = in_dim / 256;
-  const int per = (nsb + cfg.splits - 1) / cfg.splits;
-  const int real_splits = (nsb + per - 1) / per;
-  return real_splits > 1 ? (size_t)real_splits * out_dim : 0;
 }
 
 template <int KIND>
 static hipError_t launch_mv_kind(const uint8_t* W, int in_dim, int out_dim, const float* x, const float* xq,
-                                 float* y, hipStream_t s, const MvConfig& cfg, float* part) {
+                                 float* y, hipStream_t s, const MvConfig& cfg) {
   const int nsb = in_dim / 256;
+  if (nsb < 1 || nsb > 16 * 16) return hipErrorInvalidValue;
   const size_t row_bytes = (size_t)nsb * Block<KIND>::BYTES;
-  if (cfg.layout == MvLayout::Lanes) {
-    const int nsplit = cfg.splits > 0 ? cfg.splits : 1;
-    const int per = (nsb + nsplit - 1) / nsplit;
-    const int real_splits = (nsb + per - 1) / per;
-    const int waves = (out_dim + 63) / 64;
-    dim3 grid((waves + 3) / 4, real_splits);
-    float* dst = real_splits == 1 ? y : part;
-    hipLaunchKernelGGL(kq_mv_lanes<KIND>, grid, dim3(256), 0, s, W, row_bytes, nsb, out_dim, per, x, xq, dst);
-    if (real_splits > 1)
-      hipLaunchKernelGGL(kq_mv_reduce, dim3((out_dim + 255) / 256), dim3(256), 0, s, part, real_splits,
-                         out_dim, y);
-    return hipGetLastError();
-  }
+  int spl_log2, nw;
+  stream_shape(nsb, spl_log2, nw);
   const int R = cfg.rows_per_wave;
-#define KQ_LAUNCH_R(RR)                                                                         \
-  if (R == RR) {                                                                                \
-    const int waves = (out_dim + RR - 1) / RR;                                                  \
-    hipLaunchKernelGGL((kq_mv_coal<KIND, RR>), dim3((waves + 3) / 4), dim3(256), 0, s, W,       \
-                       row_bytes, nsb, out_dim, x, xq, y);                                      \
-    return hipGetLastError();                                                                   \
+  const int rows_step = (64 >> (spl_log2 + 2)) * R;
+  const int nblk = (out_dim + rows_step - 1) / rows_step;
+  // One-wave teams share 256-thread workgroups; a multi-wave team has a
+  // workgroup to itself, so its barriers only ever wait for its own waves.
+  const int tpw = nw == 1 ? 4 : 1;
+  const int threads = 64 * nw * tpw;
+  int nteams = num_cus() * max(1, cfg.waves_per_cu / nw);
+  nteams = min(nteams, nblk);
+  nteams = (nteams + tpw - 1) / tpw * tpw;
+  const int grid = nteams / tpw;
+#define KQ_STREAM_R(RR)                                                                              \
+  if (R == RR) {                                                                                     \
+    hipLaunchKernelGGL((kq_mv_stream<KIND, RR>), dim3(grid), dim3(threads), 0, s, W, row_bytes, nsb, \
+                       out_dim, x, xq, y, spl_log2, nw, nteams);                                     \
+    return hipGetLastError();                                                                        \
   }
-  KQ_LAUNCH_R(1) KQ_LAUNCH_R(2) KQ_LAUNCH_R(4) KQ_LAUNCH_R(8)
-#undef KQ_LAUNCH_R
+  KQ_STREAM_R(1) KQ_STREAM_R(2) KQ_STREAM_R(4)
+#undef KQ_STREAM_R
   return hipErrorInvalidValue;
 }
 
@@ -299,15 +325,15 @@ hipError_t launch_xsum(const float* x, int in_dim, int rows, float* xq, hipStrea
 }
 
 hipError_t launch_matvec(int kind, const void* W, int in_dim, int out_dim, const float* x, const float* xq,
-                         float* y, hipStream_t s, const MvConfig& cfg, float* part) {
+                         float* y, hipStream_t s, const MvConfig& cfg) {
   const uint8_t* w = (const uint8_t*)W;
   switch (kind) {
-    case Q4_K: return launch_mv_kind<Q4_K>(w, in_dim, out_dim, x, xq, y, s, cfg, part);
-    case Q6_K: return launch_mv_kind<Q6_K>(w, in_dim, out_dim, x, xq, y, s, cfg, part);
-    case Q5_K: return launch_mv_kind<Q5_K>(w, in_dim, out_dim, x, xq, y, s, cfg, part);
-    case Q3_K: return launch_mv_kind<Q3_K>(w, in_dim, out_dim, x, xq, y, s, cfg, part);
-    case Q2_K: return launch_mv_kind<Q2_K>(w, in_dim, out_dim, x, xq, y, s, cfg, part);
-    case Q8_0: return launch_mv_kind<Q8_0>(w, in_dim, out_dim, x, xq, y, s, cfg, part);
+    case Q4_K: return launch_mv_kind<Q4_K>(w, in_dim, out_dim, x, xq, y, s, cfg);
+    case Q6_K: return launch_mv_kind<Q6_K>(w, in_dim, out_dim, x, xq, y, s, cfg);
+    case Q5_K: return launch_mv_kind<Q5_K>(w, in_dim, out_dim, x, xq, y, s, cfg);
+    case Q3_K: return launch_mv_kind<Q3_K>(w, in_dim, out_dim, x, xq, y, s, cfg);
+    case Q2_K: return launch_mv_kind<Q2_K>(w, in_dim, out_dim, x, xq, y, s, cfg);
+    case Q8_0: return launch_mv_kind<Q8_0>(w, in_dim, out_dim, x, xq, y, s, cfg);
     default: return hipErrorInvalidValue;
   }
 }
@@ -318,7 +344,7 @@ static hipError_t launch_mm_kind(const uint8_t* W, int in_dim, int out_dim, int 
   const int nsb = in_dim / 256;
   const size_t row_bytes = (size_t)nsb * Block<KIND>::BYTES;
   const int waves = (out_dim + 3) / 4;
-  hipLaunchKernelGGL((kq_mm_coal<KIND, 4>), dim3((waves + 3) / 4), dim3(256), 0, s, W, row_bytes, nsb,
+  hipLaunchKernelGGL((kq_mm_valu<KIND, 4>), dim3((waves + 3) / 4), dim3(256), 0, s, W, row_bytes, nsb,
                      in_dim, out_dim, batch, X, XQ, Y);
   return hipGetLastError();
 }

@@ -62,9 +62,9 @@ __global__ __launch_bounds__(256) void moe_proj(ProjJob J, const float* __restri
   for (int sb = slot; sb < nsb; sb += 16) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      acc[r] += Block<KIND>::quarter(W + (size_t)min(row0 + r, J.out_rows - 1) * row_bytes +
+      acc[r] += quarter<KIND>(W + (size_t)min(row0 + r, J.out_rows - 1) * row_bytes +
                                          (size_t)sb * Block<KIND>::BYTES,
-                                     c, x + (size_t)sb * 256, xq + (size_t)sb * 16);
+                                c, x + (size_t)sb * 256, xq + (size_t)sb * 16);
   }
   float* y = J.y + (long)t * J.y_tok + (long)k * J.y_slot;
 #pragma unroll

@@ -126,11 +126,10 @@ int aspida_moe_experts_dev(const float *x, int T, int dim, int top_k, int interm
                            const void *shd_w, int shd_kind, const float *shared_gate_inp,
                            float *work, float *y, void *stream);
 
-/* Launch-shape override for batch-1 matvecs: layout 0 = coalesced (four lanes
- * per super-block, rows_per_wave in {1, 2, 4, 8}), 1 = one row per lane with
- * the super-blocks split `splits` ways; layout -1 restores the built-in
- * choice.  Process-wide; for tuning and tests. */
-int aspida_kq_set_mv_config(int layout, int rows_per_wave, int splits);
+/* Launch-shape override for batch-1 matvecs: rows per lane group per step
+ * (1, 2 or 4) and resident waves launched per CU (1..64); rows_per_wave <= 0
+ * restores the built-in choice.  Process-wide; for tuning and tests. */
+int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu);
 
 #ifdef __cplusplus
 }

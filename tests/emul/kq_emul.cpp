@@ -1,0 +1,56 @@
+// Host (x86) build of the device block math in aspida_amd/csrc/kq_blocks.h,
+// for CPU tests of the kernels' arithmetic against the oracle.  The few AMDGPU
+// builtins the block functions use are given their documented semantics here;
+// everything else (the f16-subnormal codes, the factorized sums) is the same
+// source the GPU compiles.
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#define KQ_HOST_EMULATION 1
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __shared__
+
+static inline uint32_t __builtin_amdgcn_ubfe(uint32_t v, uint32_t off, uint32_t w) {
+  off &= 31; w &= 31;
+  return w == 0 ? 0u : (v >> off) & ((1u << w) - 1u);
+}
+static inline int32_t __builtin_amdgcn_sbfe(int32_t v, uint32_t off, uint32_t w) {
+  off &= 31; w &= 31;
+  if (w == 0) return 0;
+  uint32_t u = ((uint32_t)v >> off) & ((1u << w) - 1u);
+  return (u >> (w - 1)) ? (int32_t)(u | ~((1u << w) - 1u)) : (int32_t)u;
+}
+static inline uint32_t __builtin_amdgcn_alignbit(uint32_t a, uint32_t b, uint32_t s) {
+  return (uint32_t)((((uint64_t)a << 32) | b) >> (s & 31));
+}
+struct uint2 { uint32_t x, y; };
+struct uint4 { uint32_t x, y, z, w; };
+using std::max;
+using std::min;
+
+#include "../../aspida_amd/csrc/kq_blocks.h"
+
+extern "C" float kq_emul_quarter(int kind, const uint8_t* sb, int c, const float* xs, const float* xq) {
+  switch (kind) {
+    case kq::Q4_K: return kq::quarter<kq::Q4_K>(sb, c, xs, xq);
+    case kq::Q6_K: return kq::quarter<kq::Q6_K>(sb, c, xs, xq);
+    case kq::Q5_K: return kq::quarter<kq::Q5_K>(sb, c, xs, xq);
+    case kq::Q3_K: return kq::quarter<kq::Q3_K>(sb, c, xs, xq);
+    case kq::Q2_K: return kq::quarter<kq::Q2_K>(sb, c, xs, xq);
+    case kq::Q8_0: return kq::quarter<kq::Q8_0>(sb, c, xs, xq);
+  }
+  return NAN;
+}
+
+// The aligned-load helpers on their own: 16 / 12 bytes at p.
+extern "C" void kq_emul_ld16e(const uint8_t* p, uint8_t* out) {
+  const uint4 v = kq::ld16e(p);
+  std::memcpy(out, &v, 16);
+}
+extern "C" void kq_emul_ld12e(const uint8_t* p, uint8_t* out) {
+  const uint4 v = kq::ld12e(p);
+  std::memcpy(out, &v, 12);
+}

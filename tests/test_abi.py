@@ -95,6 +95,7 @@ def test_device_entry_points_reject_bad_arguments(lib):
     assert lib.aspida_kq_matmul_dev(0, 1, 300, 1, 2, 1, 1, 1, None) < 0
     assert lib.aspida_kq_dequant_dev(0, 1, 256, 0, 1, None) < 0
     assert lib.aspida_moe_route_dev(None, 128, 2048, 1, 8, None, None, None, None, None) < 0
-    assert lib.aspida_kq_set_mv_config(0, 3, 1) < 0
-    assert lib.aspida_kq_set_mv_config(2, 4, 1) < 0
+    assert lib.aspida_kq_set_mv_config(3, 16) < 0
+    assert lib.aspida_kq_set_mv_config(2, 0) < 0
+    assert lib.aspida_kq_set_mv_config(0, 16) == 0
     assert lib.aspida_moe_work_floats(1, 2048, 8, 768) > 9 * 768 * 3

@@ -25,7 +25,7 @@ def gpu():
     torch_cuda()
     g = aa.LLMGpu()
     yield g
-    g.lib.aspida_kq_set_mv_config(-1, 4, 1)
+    g.lib.aspida_kq_set_mv_config(0, 16)
 
 
 @pytest.fixture(scope="module")
@@ -78,19 +78,22 @@ def _check_mv(gpu, kind, out_dim, in_dim, seed, what, specials=False):
     return assert_close_scaled(y, want, scale, what=what)
 
 
-SMALL_SHAPES = [(1, 256), (3, 512), (67, 1024), (130, 4096), (257, 2304)]
-LAYOUTS = [(0, 1, 1), (0, 2, 1), (0, 4, 1), (0, 8, 1), (1, 4, 1), (1, 4, 3), (1, 4, 16)]
+# Row lengths of 1..56 super-blocks exercise every stream shape: chunks of
+# 16/8/4/2/1 super-blocks per wave, teams of 1..7 waves, idle lanes.
+SMALL_SHAPES = [(1, 256), (3, 512), (67, 768), (130, 4096), (257, 2304), (33, 3328), (70, 8192),
+                (41, 14336)]
+CONFIGS = [(1, 16), (2, 16), (4, 16), (2, 4), (4, 64)]
 
 
-@pytest.mark.parametrize("layout", LAYOUTS, ids=lambda l: f"L{l[0]}R{l[1]}S{l[2]}")
+@pytest.mark.parametrize("cfg", CONFIGS, ids=lambda c: f"R{c[0]}W{c[1]}")
 @pytest.mark.parametrize("kind", KINDS)
-def test_matvec_small_shapes_all_layouts(kind, layout, gpu):
-    assert gpu.lib.aspida_kq_set_mv_config(*layout) == 0
+def test_matvec_small_shapes_all_configs(kind, cfg, gpu):
+    assert gpu.lib.aspida_kq_set_mv_config(*cfg) == 0
     try:
         for i, (out_dim, in_dim) in enumerate(SMALL_SHAPES):
             _check_mv(gpu, kind, out_dim, in_dim, 1000 * kind + i, f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
     finally:
-        gpu.lib.aspida_kq_set_mv_config(-1, 4, 1)
+        gpu.lib.aspida_kq_set_mv_config(0, 16)
 
 
 @pytest.mark.parametrize("kind", KINDS)
