@@ -216,10 +216,12 @@ template <> struct Block<Q6_K> {
     }
     // int8 scales sc[8h + t + 2k]: dword 2h holds k = 0, 1; dword 2h+1 holds k = 2, 3.
     const uint32_t sw0 = hh ? wb.s.z : wb.s.x, sw1 = hh ? wb.s.w : wb.s.y;
-    const float c1 = (float)__builtin_amdgcn_sbfe(sw0, 8 * t, 8);
-    const float c2 = (float)__builtin_amdgcn_sbfe(sw0, 8 * t + 16, 8);
-    const float c3 = (float)__builtin_amdgcn_sbfe(sw1, 8 * t, 8);
-    const float c4 = (float)__builtin_amdgcn_sbfe(sw1, 8 * t + 16, 8);
+    // v_bfe_i32 sign-extends, but the builtin's result type is unsigned:
+    // convert from int32_t.
+    const float c1 = (float)(int32_t)__builtin_amdgcn_sbfe(sw0, 8 * t, 8);
+    const float c2 = (float)(int32_t)__builtin_amdgcn_sbfe(sw0, 8 * t + 16, 8);
+    const float c3 = (float)(int32_t)__builtin_amdgcn_sbfe(sw1, 8 * t, 8);
+    const float c4 = (float)(int32_t)__builtin_amdgcn_sbfe(sw1, 8 * t + 16, 8);
     // The codes are stored offset by 32: sum (q-32) x = sum q x - 32 sum x.
     const float k32 = 32.f / 16777216.f;
     float r = (d * c1) * (a1 - k32 * x.s[0]);

@@ -36,14 +36,15 @@ __global__ void xsum16(const float* __restrict__ x, int n16, int rows, float* __
 // shuffles; with nw > 1 the team's partial sums meet in LDS (one team per
 // workgroup then, so the barriers see identical trip counts).
 constexpr int STREAM_MAX_ROWS_STEP = 64;
+constexpr int STREAM_MAX_TEAM = 8;  // waves per team (workgroup <= 512 threads)
 
 template <int KIND, int R>
-__global__ __launch_bounds__(256) void kq_mv_stream(const uint8_t* __restrict__ W, size_t row_bytes,
+__global__ __launch_bounds__(512) void kq_mv_stream(const uint8_t* __restrict__ W, size_t row_bytes,
                                                     int nsb, int out_rows, const float* __restrict__ x,
                                                     const float* __restrict__ xq, float* __restrict__ y,
                                                     int spl_log2, int nw, int nteams) {
   using B = Block<KIND>;
-  __shared__ float red[16 * STREAM_MAX_ROWS_STEP];
+  __shared__ float red[STREAM_MAX_TEAM * STREAM_MAX_ROWS_STEP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int tpw = (int)(blockDim.x >> 6) / nw;
   const int w = wv % nw;
@@ -264,18 +265,20 @@ static int num_cus() {
 
 // Chunk of super-blocks per wave (a power of two <= 16) and waves per team
 // for rows of nsb super-blocks: the chunk that leaves the fewest lanes idle,
-// the larger one on ties, with at most 16 waves per team.
-void stream_shape(int nsb, int& spl_log2, int& nw) {
+// the larger one on ties, with at most STREAM_MAX_TEAM waves per team.
+// Returns false when nsb exceeds 16 * STREAM_MAX_TEAM.
+bool stream_shape(int nsb, int& spl_log2, int& nw) {
   double best = -1.0;
   spl_log2 = 0;
-  nw = nsb;
+  nw = 0;
   for (int l = 4; l >= 0; --l) {
     const int spl = 1 << l;
     const int n = (nsb + spl - 1) / spl;
-    if (n > 16) continue;
+    if (n > STREAM_MAX_TEAM) continue;
     const double eff = (double)nsb / (double)(n * spl);
     if (eff > best + 1e-9) { best = eff; spl_log2 = l; nw = n; }
   }
+  return nw > 0;
 }
 
 MvConfig default_mv_config(int kind, int in_dim, int out_dim) {
@@ -292,10 +295,16 @@ template <int KIND>
 static hipError_t launch_mv_kind(const uint8_t* W, int in_dim, int out_dim, const float* x, const float* xq,
                                  float* y, hipStream_t s, const MvConfig& cfg) {
   const int nsb = in_dim / 256;
-  if (nsb < 1 || nsb > 16 * 16) return hipErrorInvalidValue;
   const size_t row_bytes = (size_t)nsb * Block<KIND>::BYTES;
   int spl_log2, nw;
-  stream_shape(nsb, spl_log2, nw);
+  if (nsb < 1) return hipErrorInvalidValue;
+  if (!stream_shape(nsb, spl_log2, nw)) {
+    // Rows longer than 32768 elements: the vector-ALU product with one row.
+    const int waves = (out_dim + 3) / 4;
+    hipLaunchKernelGGL((kq_mm_valu<KIND, 4>), dim3((waves + 3) / 4), dim3(256), 0, s, W, row_bytes, nsb,
+                       in_dim, out_dim, 1, x, xq, y);
+    return hipGetLastError();
+  }
   const int R = cfg.rows_per_wave;
   const int rows_step = (64 >> (spl_log2 + 2)) * R;
   const int nblk = (out_dim + rows_step - 1) / rows_step;

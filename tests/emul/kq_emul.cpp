@@ -17,11 +17,13 @@ static inline uint32_t __builtin_amdgcn_ubfe(uint32_t v, uint32_t off, uint32_t 
   off &= 31; w &= 31;
   return w == 0 ? 0u : (v >> off) & ((1u << w) - 1u);
 }
-static inline int32_t __builtin_amdgcn_sbfe(int32_t v, uint32_t off, uint32_t w) {
+// Result type as the device builtin declares it (unsigned), so a missing
+// signed conversion in the kernel source shows up here too.
+static inline uint32_t __builtin_amdgcn_sbfe(uint32_t v, uint32_t off, uint32_t w) {
   off &= 31; w &= 31;
   if (w == 0) return 0;
-  uint32_t u = ((uint32_t)v >> off) & ((1u << w) - 1u);
-  return (u >> (w - 1)) ? (int32_t)(u | ~((1u << w) - 1u)) : (int32_t)u;
+  uint32_t u = (v >> off) & ((1u << w) - 1u);
+  return (u >> (w - 1)) ? (u | ~((1u << w) - 1u)) : u;
 }
 static inline uint32_t __builtin_amdgcn_alignbit(uint32_t a, uint32_t b, uint32_t s) {
   return (uint32_t)((((uint64_t)a << 32) | b) >> (s & 31));
