@@ -34,10 +34,13 @@ namespace kq {
 
 // 16 bytes at an even address p, using only dword-aligned loads.  When p % 4
 // == 2 this also reads bytes p+16 and p+17.
+// The aligned base is formed by pointer arithmetic on p (not through an
+// integer), so the compiler keeps the global address space and emits global
+// (not flat) loads whose completion it can count precisely.
 __device__ __forceinline__ uint4 ld16e(const uint8_t* p) {
-  const uintptr_t a = (uintptr_t)p;
-  const uint8_t* q = (const uint8_t*)(a & ~(uintptr_t)3);
-  const uint32_t sh = (uint32_t)(a & 3) * 8;
+  const uint32_t mis = (uint32_t)((uintptr_t)p & 3);
+  const uint8_t* q = p - mis;
+  const uint32_t sh = mis * 8;
   uint4 v;
   __builtin_memcpy(&v, __builtin_assume_aligned(q, 4), 16);
   uint32_t e;
@@ -53,9 +56,9 @@ __device__ __forceinline__ uint4 ld16e(const uint8_t* p) {
 // 12 bytes at an even address p (returned in x, y, z), reading only the
 // dwords that overlap [p, p+12).
 __device__ __forceinline__ uint4 ld12e(const uint8_t* p) {
-  const uintptr_t a = (uintptr_t)p;
-  const uint8_t* q = (const uint8_t*)(a & ~(uintptr_t)3);
-  const uint32_t sh = (uint32_t)(a & 3) * 8;
+  const uint32_t mis = (uint32_t)((uintptr_t)p & 3);
+  const uint8_t* q = p - mis;
+  const uint32_t sh = mis * 8;
   uint32_t v0, v1, v2, v3;
   __builtin_memcpy(&v0, __builtin_assume_aligned(q, 4), 4);
   __builtin_memcpy(&v1, __builtin_assume_aligned(q + 4, 4), 4);

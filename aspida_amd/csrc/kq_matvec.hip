@@ -33,18 +33,48 @@ __global__ void xsum16(const float* __restrict__ x, int n16, int rows, float* __
 // launch; the team then walks row blocks blk = team, team + nteams, ... with
 // R rows per lane-group per step, prefetching the next block's weights before
 // computing the current one.  The lanes of a row are reduced with xor
-// shuffles; with nw > 1 the team's partial sums meet in LDS (one team per
-// workgroup then, so the barriers see identical trip counts).
+// shuffles; with nw > 1 (MULTI) the team's partial sums meet in LDS, one team
+// per workgroup so the barriers see identical trip counts.
+//
+// Every load is issued unconditionally (indices are clamped to valid rows and
+// the last prefetch repeats the final block), so the compiler's memory
+// wait counts stay static and a step waits only for its own block's bytes.
 constexpr int STREAM_MAX_ROWS_STEP = 64;
 constexpr int STREAM_MAX_TEAM = 8;  // waves per team (workgroup <= 512 threads)
 
-template <int KIND, int R>
+// Workgroup barrier ordering LDS only: it does not wait for outstanding
+// global loads, so prefetched weights stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int L>
+__device__ __forceinline__ float row_sum_pow2(float v) {
+#pragma unroll
+  for (int o = 1; o < (1 << L); o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Sum over the 2^lpr_log2 lanes of an aligned group; lpr_log2 is wave-uniform.
+__device__ __forceinline__ float row_sum(float v, int lpr_log2) {
+  switch (lpr_log2) {
+    case 2: return row_sum_pow2<2>(v);
+    case 3: return row_sum_pow2<3>(v);
+    case 4: return row_sum_pow2<4>(v);
+    case 5: return row_sum_pow2<5>(v);
+    default: return row_sum_pow2<6>(v);
+  }
+}
+
+template <int KIND, int R, bool MULTI>
 __global__ __launch_bounds__(512) void kq_mv_stream(const uint8_t* __restrict__ W, size_t row_bytes,
                                                     int nsb, int out_rows, const float* __restrict__ x,
                                                     const float* __restrict__ xq, float* __restrict__ y,
                                                     int spl_log2, int nw, int nteams) {
   using B = Block<KIND>;
-  __shared__ float red[STREAM_MAX_TEAM * STREAM_MAX_ROWS_STEP];
+  __shared__ float red[MULTI ? STREAM_MAX_TEAM * STREAM_MAX_ROWS_STEP : 1];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int tpw = (int)(blockDim.x >> 6) / nw;
   const int w = wv % nw;
@@ -54,30 +84,31 @@ __global__ __launch_bounds__(512) void kq_mv_stream(const uint8_t* __restrict__ 
   const int within = lane & ((1 << lpr_log2) - 1);
   const int c = within & 3;
   const int sb = (w << spl_log2) + (within >> 2);
-  const bool active = sb < nsb;
-  const int sbc = active ? sb : nsb - 1;
+  const float live = sb < nsb ? 1.f : 0.f;
+  const int sbc = sb < nsb ? sb : nsb - 1;
   const int rows_step = (64 >> lpr_log2) * R;
   const int nblk = (out_rows + rows_step - 1) / rows_step;
+  const int nsteps = team < nblk ? (nblk - team + nteams - 1) / nteams : 0;
+  if (nsteps == 0) return;  // uniform over the team
 
   XQuarter xf;
   B::load_x(x + (size_t)sbc * 256, xq + (size_t)sbc * 16, c, xf);
   const uint8_t* wcol = W + (size_t)sbc * B::BYTES;
 
   typename B::W buf0[R], buf1[R];
-  auto load = [&](int blk, typename B::W* dst) {
+  auto load = [&](int i, typename B::W* dst) {
+    const int blk = team + min(i, nsteps - 1) * nteams;
     const int r0 = blk * rows_step + rslot * R;
 #pragma unroll
     for (int j = 0; j < R; ++j) dst[j] = B::load_w(wcol + (size_t)min(r0 + j, out_rows - 1) * row_bytes, c);
   };
-  auto compute = [&](int blk, const typename B::W* cur) {
+  auto compute = [&](int i, const typename B::W* cur) {
+    const int blk = team + i * nteams;
     float acc[R];
 #pragma unroll
-    for (int j = 0; j < R; ++j) acc[j] = active ? B::dot(cur[j], c, xf) : 0.f;
-#pragma unroll
-    for (int j = 0; j < R; ++j)
-      for (int o = 1; o < (1 << lpr_log2); o <<= 1) acc[j] += __shfl_xor(acc[j], o, 64);
-    const int r0 = blk * rows_step + rslot * R;
-    if (nw == 1) {
+    for (int j = 0; j < R; ++j) acc[j] = row_sum(live * B::dot(cur[j], c, xf), lpr_log2);
+    if (!MULTI) {
+      const int r0 = blk * rows_step + rslot * R;
       if (within == 0) {
 #pragma unroll
         for (int j = 0; j < R; ++j)
@@ -88,27 +119,24 @@ __global__ __launch_bounds__(512) void kq_mv_stream(const uint8_t* __restrict__ 
 #pragma unroll
         for (int j = 0; j < R; ++j) red[w * rows_step + rslot * R + j] = acc[j];
       }
-      __syncthreads();
+      lds_barrier();
       if ((int)threadIdx.x < rows_step) {
         float s = 0.f;
         for (int k = 0; k < nw; ++k) s += red[k * rows_step + threadIdx.x];
         const int r = blk * rows_step + threadIdx.x;
         if (r < out_rows) y[r] = s;
       }
-      __syncthreads();
+      lds_barrier();
     }
   };
-  int blk = team;
-  if (blk < nblk) load(blk, buf0);
-  while (blk < nblk) {
-    const int b1 = blk + nteams;
-    if (b1 < nblk) load(b1, buf1);
-    compute(blk, buf0);
-    if (b1 >= nblk) break;
-    const int b2 = b1 + nteams;
-    if (b2 < nblk) load(b2, buf0);
-    compute(b1, buf1);
-    blk = b2;
+  load(0, buf0);
+  for (int i = 0;; i += 2) {
+    load(i + 1, buf1);
+    compute(i, buf0);
+    if (i + 1 >= nsteps) break;
+    load(i + 2, buf0);
+    compute(i + 1, buf1);
+    if (i + 2 >= nsteps) break;
   }
 }
 
@@ -316,11 +344,15 @@ static hipError_t launch_mv_kind(const uint8_t* W, int in_dim, int out_dim, cons
   nteams = min(nteams, nblk);
   nteams = (nteams + tpw - 1) / tpw * tpw;
   const int grid = nteams / tpw;
-#define KQ_STREAM_R(RR)                                                                              \
-  if (R == RR) {                                                                                     \
-    hipLaunchKernelGGL((kq_mv_stream<KIND, RR>), dim3(grid), dim3(threads), 0, s, W, row_bytes, nsb, \
-                       out_dim, x, xq, y, spl_log2, nw, nteams);                                     \
-    return hipGetLastError();                                                                        \
+#define KQ_STREAM_R(RR)                                                                             \
+  if (R == RR) {                                                                                    \
+    if (nw == 1)                                                                                    \
+      hipLaunchKernelGGL((kq_mv_stream<KIND, RR, false>), dim3(grid), dim3(threads), 0, s, W,       \
+                         row_bytes, nsb, out_dim, x, xq, y, spl_log2, nw, nteams);                  \
+    else                                                                                            \
+      hipLaunchKernelGGL((kq_mv_stream<KIND, RR, true>), dim3(grid), dim3(threads), 0, s, W,        \
+                         row_bytes, nsb, out_dim, x, xq, y, spl_log2, nw, nteams);                  \
+    return hipGetLastError();                                                                       \
   }
   KQ_STREAM_R(1) KQ_STREAM_R(2) KQ_STREAM_R(4)
 #undef KQ_STREAM_R
