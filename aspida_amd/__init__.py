@@ -57,6 +57,10 @@ def load(path=None):
         "aspida_kq_xsum_dev": (I, [P, I, I, P, P]),
         "aspida_kq_matvec_dev": (I, [I, P, I, I, P, P, P, P]),
         "aspida_kq_matmul_dev": (I, [I, P, I, I, I, P, P, P, P]),
+        "aspida_kq_packed_bytes": (ctypes.c_longlong, [I, I, I]),
+        "aspida_kq_pack_dev": (I, [I, P, I, I, P, P]),
+        "aspida_kq_unpack_dev": (I, [I, P, I, I, P, P]),
+        "aspida_kq_matvec_packed_dev": (I, [I, P, I, I, P, P, P]),
         "aspida_kq_matmul_valu_dev": (I, [I, P, I, I, I, P, P, P, P]),
         "aspida_kq_dequant_dev": (I, [I, P, I, I, P, P]),
         "aspida_dense_matvec_dev": (I, [P, I, I, P, P, P]),
@@ -78,7 +82,7 @@ def exported_symbols_declared():
     """Function names declared in include/aspidagpu.h."""
     import re
     txt = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:void|int|long)\s+(aspida_\w+)\s*\(", txt, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:void|int|long long|long)\s+(aspida_\w+)\s*\(", txt, re.M)))
 
 
 def _p(a):
@@ -158,6 +162,19 @@ class DeviceOps:
 
     def matvec(self, kind, w, in_dim, out_dim, x, xq, y, stream=0):
         self._ok(self.lib.aspida_kq_matvec_dev(kind, w, in_dim, out_dim, x, xq, y, stream), "aspida_kq_matvec_dev")
+
+    def packed_bytes(self, kind, in_dim, out_dim):
+        return int(self.lib.aspida_kq_packed_bytes(kind, in_dim, out_dim))
+
+    def pack(self, kind, w, in_dim, out_dim, packed, stream=0):
+        self._ok(self.lib.aspida_kq_pack_dev(kind, w, in_dim, out_dim, packed, stream), "aspida_kq_pack_dev")
+
+    def unpack(self, kind, packed, in_dim, out_dim, w, stream=0):
+        self._ok(self.lib.aspida_kq_unpack_dev(kind, packed, in_dim, out_dim, w, stream), "aspida_kq_unpack_dev")
+
+    def matvec_packed(self, kind, packed, in_dim, out_dim, x, y, stream=0):
+        self._ok(self.lib.aspida_kq_matvec_packed_dev(kind, packed, in_dim, out_dim, x, y, stream),
+                 "aspida_kq_matvec_packed_dev")
 
     def matmul(self, kind, w, in_dim, out_dim, batch, x, xq, y, stream=0, valu=False):
         fn = self.lib.aspida_kq_matmul_valu_dev if valu else self.lib.aspida_kq_matmul_dev

@@ -17,6 +17,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
+#include <cstdint>
 #include <mutex>
 #include <unordered_map>
 
@@ -66,8 +68,8 @@ struct WEnt {
 std::mutex g_wmu;
 std::unordered_map<const void*, WEnt> g_wcache;
 
-// Device mirror of [w, w + bytes).  A cached copy at least that large is
-// reused; a smaller one is replaced.
+// Device mirror of [w, w + bytes) in the ggml layout.  A cached copy at least
+// that large is reused; a smaller one is replaced.
 void* weight(const void* w, long bytes) {
   std::lock_guard<std::mutex> lk(g_wmu);
   auto it = g_wcache.find(w);
@@ -83,6 +85,41 @@ void* weight(const void* w, long bytes) {
     return nullptr;
   }
   g_wcache[w] = {d, bytes};
+  return d;
+}
+
+// Device mirror of the matrix at w in the lane-interleaved layout of the
+// batch-1 kernels, packed on the device from a temporary ggml copy.  Keyed by
+// host pointer; a different kind or shape for the same pointer re-packs.
+struct PEnt {
+  void* d;
+  int kind, in_dim, out_dim;
+};
+std::unordered_map<const void*, PEnt> g_pcache;
+
+void* packed_weight(const void* w, int kind, int in_dim, int out_dim) {
+  std::lock_guard<std::mutex> lk(g_wmu);
+  auto it = g_pcache.find(w);
+  if (it != g_pcache.end()) {
+    const PEnt& e = it->second;
+    if (e.kind == kind && e.in_dim == in_dim && e.out_dim == out_dim) return e.d;
+    (void)hipFree(e.d);
+    g_pcache.erase(it);
+  }
+  const size_t raw = (size_t)need_bytes(kind, in_dim, out_dim);
+  const size_t pb = kq::packed_bytes(kind, in_dim, out_dim);
+  void *tmp = nullptr, *d = nullptr;
+  int rc = check(hipMalloc(&tmp, raw), "weight upload: hipMalloc");
+  if (!rc) rc = check(hipMalloc(&d, pb), "weight upload: hipMalloc packed");
+  if (!rc) rc = check(hipMemcpy(tmp, w, raw, hipMemcpyHostToDevice), "weight upload: hipMemcpy");
+  if (!rc) rc = check(kq::launch_pack(kind, tmp, in_dim, out_dim, d, false, nullptr), "weight upload: pack");
+  if (!rc) rc = check(hipStreamSynchronize(nullptr), "weight upload: sync");
+  if (tmp) (void)hipFree(tmp);
+  if (rc) {
+    if (d) (void)hipFree(d);
+    return nullptr;
+  }
+  g_pcache[w] = {d, kind, in_dim, out_dim};
   return d;
 }
 
@@ -118,12 +155,29 @@ struct HostBuf {
   }
 };
 
+// Partial sums and per-tile arrival counters of the packed matvec
+// (kq::launch_matvec_packed).  Counters start zeroed and every launch leaves
+// them zero; launches sharing a workspace must be ordered on one stream.
+struct MvWorkspace {
+  DevBuf<float> part;
+  DevBuf<unsigned> count;
+  int ensure(int in_dim, int out_dim) {
+    if (part.ensure(std::max<size_t>(kq::packed_workspace_floats(in_dim, out_dim), 64), "hipMalloc partials"))
+      return -1;
+    const size_t want = kq::packed_counters(out_dim);
+    if (want <= count.n) return 0;
+    if (count.ensure(want, "hipMalloc counters")) return -1;
+    return check(hipMemset(count.p, 0, count.n * sizeof(unsigned)), "hipMemset counters");
+  }
+};
+
 // Buffers live until the process ends (thread exit does not release them).
 struct Ctx {
   hipStream_t st = nullptr;
   DevBuf<float> dx, dy, dq, dh;
   HostBuf<float> hx, hy;
   DevBuf<int> di;
+  MvWorkspace ws;
   int init() {
     if (st) return 0;
     return check(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
@@ -171,10 +225,10 @@ int validate_mv(const char* fn, const void* w, long wbytes, int kind, int in_dim
   return 0;
 }
 
-// x -> device (through pinned staging), per-group sums, then `launch`, then
-// y <- device; synchronous.
+// x -> device (through pinned staging), per-group sums (when `sums`), then
+// `launch`, then y <- device; synchronous.
 template <class F>
-int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int rows, F&& launch) {
+int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int rows, bool sums, F&& launch) {
   if (c.init()) return -1;
   if (c.dx.ensure((size_t)nx, "hipMalloc x") || c.dy.ensure((size_t)ny, "hipMalloc y") ||
       c.dq.ensure((size_t)(nx / 16 + 1), "hipMalloc xsum") || c.hx.ensure((size_t)nx, "pinned x") ||
@@ -183,7 +237,7 @@ int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int
   std::memcpy(c.hx.p, x, (size_t)nx * sizeof(float));
   if (check(hipMemcpyAsync(c.dx.p, c.hx.p, (size_t)nx * sizeof(float), hipMemcpyHostToDevice, c.st), "H2D x"))
     return -1;
-  if (check(kq::launch_xsum(c.dx.p, in_dim, rows, c.dq.p, c.st), "xsum launch")) return -1;
+  if (sums && check(kq::launch_xsum(c.dx.p, in_dim, rows, c.dq.p, c.st), "xsum launch")) return -1;
   if (check(launch(), "kernel launch")) return -1;
   if (check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)ny * sizeof(float), hipMemcpyDeviceToHost, c.st), "D2H y"))
     return -1;
@@ -204,15 +258,14 @@ extern "C" void aspida_gpu_matvec(const void* w, long wbytes, int kind, int in_d
     fill_nan(y, out_dim);
     return;
   }
-  void* dw = weight(w, need_bytes(kind, in_dim, out_dim));
+  void* dw = packed_weight(w, kind, in_dim, out_dim);
   Ctx& c = ctx();
   int rc = dw ? 0 : -1;
-  if (!rc) {
-    const kq::MvConfig cfg = mv_config(kind, in_dim, out_dim);
-    rc = run_host(c, x, in_dim, y, out_dim, in_dim, 1, [&]() {
-      return kq::launch_matvec(kind, dw, in_dim, out_dim, c.dx.p, c.dq.p, c.dy.p, c.st, cfg);
+  if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim) ? -1 : 0;
+  if (!rc)
+    rc = run_host(c, x, in_dim, y, out_dim, in_dim, 1, false, [&]() {
+      return kq::launch_matvec_packed(kind, dw, in_dim, out_dim, c.dx.p, c.dy.p, c.ws.part.p, c.ws.count.p, c.st);
     });
-  }
   if (rc) fill_nan(y, out_dim);
 }
 
@@ -227,7 +280,7 @@ extern "C" void aspida_gpu_matmul(const void* w, long wbytes, int kind, int in_d
   Ctx& c = ctx();
   int rc = dw ? 0 : -1;
   if (!rc)
-    rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, [&]() {
+    rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, true, [&]() {
       hipError_t e = kq::launch_matmul_mfma(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.st);
       if (e == hipErrorNotSupported)
         e = kq::launch_matmul_valu(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dq.p, c.dy.p, c.st);
@@ -265,9 +318,15 @@ extern "C" void aspida_gpu_dense_matvec(const void* w, long wbytes, int in_dim, 
 extern "C" void aspida_gpu_free_weight(const void* w) {
   std::lock_guard<std::mutex> lk(g_wmu);
   auto it = g_wcache.find(w);
-  if (it == g_wcache.end()) return;
-  (void)hipFree(it->second.d);
-  g_wcache.erase(it);
+  if (it != g_wcache.end()) {
+    (void)hipFree(it->second.d);
+    g_wcache.erase(it);
+  }
+  auto pt = g_pcache.find(w);
+  if (pt != g_pcache.end()) {
+    (void)hipFree(pt->second.d);
+    g_pcache.erase(pt);
+  }
 }
 
 extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int intermed, int n_exp,
@@ -371,6 +430,46 @@ extern "C" int aspida_kq_matvec_dev(int kind, const void* w, int in_dim, int out
   const kq::MvConfig cfg = mv_config(kind, in_dim, out_dim);
   return check(kq::launch_matvec(kind, w, in_dim, out_dim, x, xq, y, (hipStream_t)stream, cfg),
                "aspida_kq_matvec_dev");
+}
+
+extern "C" long long aspida_kq_packed_bytes(int kind, int in_dim, int out_dim) {
+  if (!valid_kind(kind)) return 0;
+  return (long long)kq::packed_bytes(kind, in_dim, out_dim);
+}
+
+extern "C" int aspida_kq_pack_dev(int kind, const void* w, int in_dim, int out_dim, void* packed, void* stream) {
+  if (!w || !packed || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
+  return check(kq::launch_pack(kind, w, in_dim, out_dim, packed, false, (hipStream_t)stream), "aspida_kq_pack_dev");
+}
+
+extern "C" int aspida_kq_unpack_dev(int kind, const void* packed, int in_dim, int out_dim, void* w, void* stream) {
+  if (!w || !packed || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
+  return check(kq::launch_pack(kind, packed, in_dim, out_dim, w, true, (hipStream_t)stream),
+               "aspida_kq_unpack_dev");
+}
+
+namespace {
+// Packed-matvec workspaces of the device entry point, one per stream.
+std::mutex g_ws_mu;
+std::unordered_map<void*, MvWorkspace*> g_ws;
+}  // namespace
+
+extern "C" int aspida_kq_matvec_packed_dev(int kind, const void* packed, int in_dim, int out_dim, const float* x,
+                                           float* y, void* stream) {
+  if (!packed || !x || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 ||
+      ((uintptr_t)x & 15))
+    return -EINVAL;
+  MvWorkspace* ws;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    MvWorkspace*& slot = g_ws[stream];
+    if (!slot) slot = new MvWorkspace();
+    ws = slot;
+    if (ws->ensure(in_dim, out_dim)) return t_last_error ? t_last_error : -1;
+  }
+  return check(kq::launch_matvec_packed(kind, packed, in_dim, out_dim, x, y, ws->part.p, ws->count.p,
+                                        (hipStream_t)stream),
+               "aspida_kq_matvec_packed_dev");
 }
 
 extern "C" int aspida_kq_matmul_dev(int kind, const void* w, int in_dim, int out_dim, int batch, const float* x,

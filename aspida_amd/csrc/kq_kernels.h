@@ -2,6 +2,7 @@
 // All launchers are asynchronous on the given stream and allocate nothing.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 
 namespace kq {
 
@@ -34,5 +35,32 @@ hipError_t launch_dense(const float* W, int in_dim, int out_dim, const float* x,
 
 // dst[out][in] = dequantized W, bit-identical to the CPU decoders.
 hipError_t launch_dequant(int kind, const void* W, int in_dim, int out_dim, float* dst, hipStream_t s);
+
+// ---- lane-interleaved ("packed") layout, kq_packed.h ----
+
+// Launch split of a packed matvec: spw super-block columns per wave, nw waves
+// per workgroup, ks workgroups per 64-row tile (nw * ks * spw == in_dim / 256).
+struct PackedPlan {
+  int nw, ks, spw;
+};
+PackedPlan packed_plan(int in_dim, int out_dim);
+
+// Bytes of the packed image of a [out_dim][in_dim] matrix (rows rounded up to
+// a multiple of 64); 0 for an invalid kind or shape.
+size_t packed_bytes(int kind, int in_dim, int out_dim);
+
+// Workspace a packed matvec of this shape needs: partial sums (floats) and
+// per-tile arrival counters (unsigned, zero before the first launch; every
+// launch leaves them zero again).
+size_t packed_workspace_floats(int in_dim, int out_dim);
+size_t packed_counters(int out_dim);
+
+// ggml layout -> packed (unpack = false) or back (unpack = true).
+hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void* dst, bool unpack, hipStream_t s);
+
+// y = W x for packed W; x is 16-byte aligned.  Launches that share a
+// workspace must be ordered (one stream).
+hipError_t launch_matvec_packed(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y,
+                                float* part, unsigned* count, hipStream_t s);
 
 }  // namespace kq

@@ -1,0 +1,145 @@
+// kq_packed.h -- the lane-interleaved ("packed") HBM layout of K-quant
+// weights used by the batch-1 decode kernels, and the per-lane register
+// image of one super-block in that layout.
+//
+// A ggml row-major matrix [out][in/256 super-blocks] is regrouped into tiles
+// of 64 consecutive rows.  Tile t, super-block column s occupies 64 * BYTES
+// contiguous bytes at ((t * nsb) + s) * 64 * BYTES, holding the 64 rows'
+// super-blocks of that column:
+//   * chunk planes: byte b < 16 * C of row r (0..63) sits at
+//       (b / 16) * 1024 + r * 16 + (b % 16),
+//     so one 16-byte load per lane reads 1 KB contiguous for the wave;
+//   * tail planes: the few bytes past the last whole chunk (the f16 d of
+//     Q6_K, the scales and d of Q3_K, d/dmin of Q2_K) are stored as arrays
+//     [64][field bytes] after the chunk planes, one plane per field;
+//   * Q8_0 (eight 34-byte blocks per 256 elements) places the 32 codes of
+//     block j in chunks 2j and 2j+1 and the eight f16 scales in chunk 16.
+// The regrouping only moves bytes: every tile holds exactly 64 * BYTES bytes,
+// and rows past out_rows in the last tile are zero.  Each lane of a wave then
+// owns one row and holds its whole super-block in registers, and every lane
+// multiplies the same activations, which the kernels keep in scalar
+// registers.
+#pragma once
+#include "kq_blocks.h"
+
+namespace kq {
+
+template <int KIND> struct Packed;
+
+// Offset of byte b (0..BYTES-1) of row r's super-block inside its
+// (tile, column) group, for the formats whose only irregularity is a tail.
+// Returns -1 for bytes a format maps separately.
+__host__ __device__ constexpr int packed_offset(int kind, int r, int b) {
+  switch (kind) {
+    case Q4_K: return (b / 16) * 1024 + r * 16 + (b % 16);
+    case Q5_K: return (b / 16) * 1024 + r * 16 + (b % 16);
+    case Q6_K:
+      return b < 208 ? (b / 16) * 1024 + r * 16 + (b % 16) : 13 * 1024 + r * 2 + (b - 208);
+    case Q3_K:
+      return b < 96 ? (b / 16) * 1024 + r * 16 + (b % 16)
+                    : (b < 108 ? 6 * 1024 + r * 12 + (b - 96) : 6 * 1024 + 768 + r * 2 + (b - 108));
+    case Q2_K: return b < 80 ? (b / 16) * 1024 + r * 16 + (b % 16) : 5 * 1024 + r * 4 + (b - 80);
+    case Q8_0: {
+      const int j = b / 34, o = b % 34;
+      return o < 2 ? 16 * 1024 + r * 16 + 2 * j + o : (2 * j + (o - 2) / 16) * 1024 + r * 16 + (o - 2) % 16;
+    }
+    default: return -1;
+  }
+}
+
+// Whole-chunk loads of row `lane`'s super-block from the group at g.
+template <int C>
+__device__ __forceinline__ void load_chunks(const uint8_t* g, int lane, uint4 (&ch)[C]) {
+  const uint8_t* p = g + lane * 16;
+#pragma unroll
+  for (int k = 0; k < C; ++k) ch[k] = ld16(p + k * 1024);
+}
+
+template <> struct Packed<Q4_K> {
+  struct R { uint4 ch[9]; };
+  __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
+    R r;
+    load_chunks<9>(g, lane, r.ch);
+    return r;
+  }
+  __device__ static __forceinline__ Block<Q4_K>::W quarter(const R& r, int q) {
+    return {r.ch[0], r.ch[1 + 2 * q], r.ch[2 + 2 * q]};
+  }
+};
+
+template <> struct Packed<Q5_K> {
+  struct R { uint4 ch[11]; };
+  __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
+    R r;
+    load_chunks<11>(g, lane, r.ch);
+    return r;
+  }
+  __device__ static __forceinline__ Block<Q5_K>::W quarter(const R& r, int q) {
+    return {r.ch[0], r.ch[1], r.ch[2], r.ch[3 + 2 * q], r.ch[4 + 2 * q]};
+  }
+};
+
+template <> struct Packed<Q6_K> {
+  struct R { uint4 ch[13]; uint32_t d; };
+  __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
+    R r;
+    load_chunks<13>(g, lane, r.ch);
+    r.d = ld2(g + 13 * 1024 + 2 * lane);
+    return r;
+  }
+  // Quarter c = 2h + t: ql bytes 64h+16t.. and 64h+32+16t.., qh bytes
+  // 128+32h+16t.., the 16 scales, d (the ggml offsets of Block<Q6_K>::load_w).
+  __device__ static __forceinline__ Block<Q6_K>::W quarter(const R& r, int c) {
+    const int h = c >> 1, t = c & 1;
+    return {r.ch[4 * h + t], r.ch[4 * h + 2 + t], r.ch[8 + 2 * h + t], r.ch[12], r.d};
+  }
+};
+
+template <> struct Packed<Q3_K> {
+  struct R { uint4 ch[6]; uint4 s; uint32_t d; };
+  __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
+    R r;
+    load_chunks<6>(g, lane, r.ch);
+    const uint8_t* sp = g + 6 * 1024 + 12 * lane;
+    r.s = make_uint4(ld4(sp), ld4(sp + 4), ld4(sp + 8), 0u);
+    r.d = ld2(g + 6 * 1024 + 768 + 2 * lane);
+    return r;
+  }
+  // Quarter c = 2nh + g: qs bytes 32+32nh+16g.., hmask bytes 16g.. (ggml offsets).
+  __device__ static __forceinline__ Block<Q3_K>::W quarter(const R& r, int c) {
+    const int nh = c >> 1, g = c & 1;
+    return {r.ch[2 + 2 * nh + g], r.ch[g], r.s, r.d};
+  }
+};
+
+template <> struct Packed<Q2_K> {
+  struct R { uint4 ch[5]; uint32_t d; };
+  __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
+    R r;
+    load_chunks<5>(g, lane, r.ch);
+    r.d = ld4(g + 5 * 1024 + 4 * lane);
+    return r;
+  }
+  // Quarter c = 2nh + g: qs bytes 16+32nh+16g.., scale bytes 8nh..8nh+7.
+  __device__ static __forceinline__ Block<Q2_K>::W quarter(const R& r, int c) {
+    const int nh = c >> 1, g = c & 1;
+    return {r.ch[1 + 2 * nh + g], nh ? make_uint2(r.ch[0].z, r.ch[0].w) : make_uint2(r.ch[0].x, r.ch[0].y), r.d};
+  }
+};
+
+template <> struct Packed<Q8_0> {
+  struct R { uint4 ch[17]; };
+  __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
+    R r;
+    load_chunks<17>(g, lane, r.ch);
+    return r;
+  }
+  // Quarter c owns blocks 2c and 2c+1: codes in chunks 4c..4c+3, scales in
+  // dword c of chunk 16.
+  __device__ static __forceinline__ Block<Q8_0>::W quarter(const R& r, int c) {
+    const uint32_t dw = c == 0 ? r.ch[16].x : c == 1 ? r.ch[16].y : c == 2 ? r.ch[16].z : r.ch[16].w;
+    return {r.ch[4 * c], r.ch[4 * c + 1], r.ch[4 * c + 2], r.ch[4 * c + 3], dw & 0xFFFFu, dw >> 16};
+  }
+};
+
+}  // namespace kq

@@ -1,0 +1,243 @@
+// kq_packed.hip -- batch-1 decode matvec over the lane-interleaved layout
+// (kq_packed.h), and the kernels that move weights into and out of it.
+//
+// kq_mv_packed: lane l of a wave owns row 64 * tile + l and walks a range of
+// super-block columns; per column it loads its row's whole super-block (one
+// 1 KB-coalesced 16-byte load per chunk plane), and all lanes multiply the
+// same 256 activations, which the compiler keeps in scalar registers
+// (s_load), so the vector registers hold only weights and accumulators.  The
+// per-16 activation sums for the min/offset terms are formed in the kernel
+// (one 16-byte load per lane, a DPP quad sum, readlane), so a matvec is a
+// single launch.
+//
+// The columns of a tile are split over the NW waves of a workgroup and over
+// `ks` workgroups (grid.y).  Waves meet in LDS; workgroups write partial
+// sums to a workspace, and the last workgroup of a tile to arrive (an atomic
+// arrival counter per tile) adds them in ascending order, writes y and
+// re-arms the counter -- so results are deterministic and the launch needs no
+// memset.
+#include <algorithm>
+
+#include "kq_packed.h"
+#include "kq_kernels.h"
+
+namespace kq {
+
+// s16[j] = sum of xs[16j .. 16j+15] for the 256 activations at xs (16-byte
+// aligned), as wave-uniform values.
+__device__ __forceinline__ void sb_sums(const float* __restrict__ xs, int lane, float (&s16)[16]) {
+  float4 v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(xs + 4 * lane, 16), 16);
+  float t = (v.x + v.y) + (v.z + v.w);
+  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, false));
+  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, false));
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s16[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 4 * j));
+}
+
+template <int KIND, int NW>
+__global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restrict__ P, int nsb, int out_rows,
+                                                       const float* __restrict__ x, float* __restrict__ y, int spw,
+                                                       float* __restrict__ part, unsigned* __restrict__ count) {
+  using B = Block<KIND>;
+  using PK = Packed<KIND>;
+  constexpr int GB = 64 * B::BYTES;
+  __shared__ float red[NW > 1 ? NW * 64 : 1];
+  __shared__ unsigned is_last;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x;
+  const int ks = gridDim.y;
+  const int sb0 = (blockIdx.y * NW + w) * spw;
+  const uint8_t* g = P + ((size_t)tile * nsb + sb0) * GB;
+  const float* xs = x + (size_t)sb0 * 256;
+  float acc = 0.f;
+  for (int s = 0; s < spw; ++s, g += GB, xs += 256) {
+    const typename PK::R r = PK::load(g, lane);
+    float s16[16];
+    sb_sums(xs, lane, s16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      XQuarter X;
+      B::load_x(xs, s16, q, X);
+      acc += B::dot(PK::quarter(r, q), q, X);
+    }
+  }
+  if (NW > 1) {
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+      float t = red[lane];
+#pragma unroll
+      for (int k = 1; k < NW; ++k) t += red[k * 64 + lane];
+      acc = t;
+    }
+  }
+  const int row = tile * 64 + lane;
+  if (ks == 1) {
+    if (w == 0 && row < out_rows) y[row] = acc;
+    return;
+  }
+  // Cross-workgroup sum.  The partials and the counter are device-scope
+  // (sc1) atomics, which bypass the per-XCD L2s, so no agent-scope fence --
+  // an L2 write-back and invalidate on this chip -- is needed: the wait
+  // below retires the partial store before the arrival is counted, and the
+  // last arrival reads the partials only after its counter update returned.
+  const size_t ntiles = gridDim.x;
+  if (w == 0)
+    __hip_atomic_store(&part[((size_t)blockIdx.y * ntiles + tile) * 64 + lane], acc, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(&count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (unsigned)(ks - 1)
+                  ? 1u
+                  : 0u;
+  __syncthreads();
+  if (is_last && w == 0) {
+    float t = 0.f;
+    for (int k = 0; k < ks; ++k)
+      t += __hip_atomic_load(&part[((size_t)k * ntiles + tile) * 64 + lane], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    if (row < out_rows) y[row] = t;
+    if (lane == 0) __hip_atomic_store(&count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Byte moves between the ggml layout W[out][nsb] and the packed layout; one
+// thread per byte of the packed image (rows past out_rows pack as zeros and
+// are skipped when unpacking).
+template <int KIND>
+__global__ void kq_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int nsb, int out_rows,
+                        size_t total, int unpack) {
+  constexpr int BB = Block<KIND>::BYTES;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+    const int b = (int)(i % BB);
+    const size_t rest = i / BB;
+    const int r = (int)(rest % 64);
+    const size_t grp = rest / 64;  // tile * nsb + sb
+    const int sb = (int)(grp % nsb);
+    const size_t tile = grp / nsb;
+    const size_t row = tile * 64 + r;
+    const size_t off_p = grp * (size_t)(64 * BB) + (size_t)packed_offset(KIND, r, b);
+    const size_t off_g = (row * nsb + sb) * BB + b;
+    if (!unpack)
+      dst[off_p] = row < (size_t)out_rows ? src[off_g] : (uint8_t)0;
+    else if (row < (size_t)out_rows)
+      dst[off_g] = src[off_p];
+  }
+}
+
+// ---- launchers --------------------------------------------------------------
+
+static int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return cus;
+}
+
+size_t packed_bytes(int kind, int in_dim, int out_dim) {
+  const int bb = block_bytes(kind);
+  if (bb <= 0 || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return 0;
+  return (size_t)((out_dim + 63) / 64) * 64 * (size_t)(in_dim / 256) * bb;
+}
+
+// Columns per wave, waves per workgroup and workgroups per tile.  A
+// workgroup of up to 16 waves covering a whole tile needs no cross-workgroup
+// sum, and is the fastest split whenever there are enough tiles to occupy
+// the chip: with >= 256 tiles the columns per wave are chosen for about 14
+// waves per CU, with >= 64 tiles and <= 16 columns every wave takes one
+// column.  Narrower matrices split each tile over ks workgroups of up to 8
+// waves (4 below 32 tiles, for more workgroups), one column per wave.
+static int pow2_divisor_upto(int n, int cap) {
+  int d = 1;
+  while (d * 2 <= cap && n % (d * 2) == 0) d *= 2;
+  return d;
+}
+
+PackedPlan packed_plan(int in_dim, int out_dim) {
+  static const int cus = device_cus();
+  const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
+  PackedPlan p{1, 1, nsb};
+  if (ntiles >= 256) {
+    const double target = 14.0 * cus;
+    double best = 1e30;
+    for (int spw = 1; spw <= nsb; ++spw) {
+      if (nsb % spw || nsb / spw > 16) continue;
+      const double waves = (double)ntiles * (nsb / spw);
+      const double miss = waves > target ? waves / target : target / waves;
+      if (miss < best - 1e-9) { best = miss; p.spw = spw; }
+    }
+    p.nw = pow2_divisor_upto(nsb / p.spw, 16);
+    p.spw = nsb / p.nw;
+    return p;
+  }
+  if (ntiles >= 64 && nsb <= 16) {
+    p.nw = pow2_divisor_upto(nsb, 16);
+    p.spw = nsb / p.nw;
+    return p;
+  }
+  p.spw = 1;
+  p.nw = pow2_divisor_upto(nsb, ntiles < 32 ? 4 : 8);
+  p.ks = nsb / p.nw;
+  return p;
+}
+
+size_t packed_workspace_floats(int in_dim, int out_dim) {
+  const PackedPlan p = packed_plan(in_dim, out_dim);
+  return p.ks > 1 ? (size_t)p.ks * ((out_dim + 63) / 64) * 64 : 0;
+}
+
+size_t packed_counters(int out_dim) { return (size_t)(out_dim + 63) / 64; }
+
+template <int KIND>
+static hipError_t launch_mvp_kind(const uint8_t* P, int in_dim, int out_dim, const float* x, float* y, float* part,
+                                  unsigned* count, hipStream_t s) {
+  const PackedPlan p = packed_plan(in_dim, out_dim);
+  const dim3 grid((out_dim + 63) / 64, p.ks);
+  const int nsb = in_dim / 256;
+  switch (p.nw) {
+#define KQ_MVP(N) \
+  case N: hipLaunchKernelGGL((kq_mv_packed<KIND, N>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw, part, count); break;
+    KQ_MVP(16) KQ_MVP(8) KQ_MVP(4) KQ_MVP(2) KQ_MVP(1)
+#undef KQ_MVP
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec_packed(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y,
+                                float* part, unsigned* count, hipStream_t s) {
+  const uint8_t* w = (const uint8_t*)P;
+  switch (kind) {
+    case Q4_K: return launch_mvp_kind<Q4_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q6_K: return launch_mvp_kind<Q6_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q5_K: return launch_mvp_kind<Q5_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q3_K: return launch_mvp_kind<Q3_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q2_K: return launch_mvp_kind<Q2_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q8_0: return launch_mvp_kind<Q8_0>(w, in_dim, out_dim, x, y, part, count, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void* dst, bool unpack, hipStream_t s) {
+  const size_t total = packed_bytes(kind, in_dim, out_dim);
+  if (total == 0) return hipErrorInvalidValue;
+  const int nsb = in_dim / 256;
+  const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, (size_t)1 << 20);
+  const uint8_t* a = (const uint8_t*)src;
+  uint8_t* b = (uint8_t*)dst;
+#define KQ_PACK(K) \
+  case K: hipLaunchKernelGGL(kq_pack<K>, dim3(blocks), dim3(256), 0, s, a, b, nsb, out_dim, total, unpack ? 1 : 0); break;
+  switch (kind) {
+    KQ_PACK(Q4_K) KQ_PACK(Q6_K) KQ_PACK(Q5_K) KQ_PACK(Q3_K) KQ_PACK(Q2_K) KQ_PACK(Q8_0)
+    default: return hipErrorInvalidValue;
+  }
+#undef KQ_PACK
+  return hipGetLastError();
+}
+
+}  // namespace kq

@@ -1,0 +1,334 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-weight hot path on one MI355X.
+
+Workload (one "step" = one decoded token): the batch-1 weight stream of a
+Llama-3-8B Q4_K_M model -- 32 layers of q, k, o, gate, up in Q4_K and v, down
+in Q6_K, plus the Q6_K output head (4,875,853,824 weight bytes per token; the
+Q4_K_M mix follows tools/probes/requantize.adb:103-113).  Each projection is a
+fused dequant+dot matvec of libaspidagpu.so on weights resident in HBM, launched
+in the decode order a layer needs them: q|k (one launch over the
+concatenated rows) and v, then o, then the gate|up launch, then down; the
+head at the end.  Weights sit in HBM in the library's packed layout (packed
+once at load, as the drop-in ABI does on upload).  Attention, norms and SwiGLU
+are not part of the path and are not run: their inputs are fixed synthetic
+activations, so the step times only the quantized matvecs.  One step is
+captured once in a HIP graph and replayed.
+
+Printed: one JSON line (metric, value = tokens/s, roofline of the dominant
+kernel measured with HIP events on its stream, cpu_baseline = the C oracle of
+Aspida's CPU QMatVec on the host cores, and the per-kind batch-1 matvec table
+at the Llama-3-8B FFN shapes on cold HBM).
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBS = 8000.0
+GIB = 1 << 30
+
+# Llama-3-8B: hidden 4096, FFN 14336, 32 q heads / 8 kv heads of 128, vocab 128256.
+HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
+Q4_K, Q6_K = 0, 1
+
+
+def layer_plan():
+    """(name, kind, out_dim, in_dim, input) per matvec launch of one layer."""
+    return [("qk", Q4_K, HIDDEN + KV, HIDDEN, "h"),
+            ("v", Q6_K, KV, HIDDEN, "h"),
+            ("o", Q4_K, HIDDEN, HIDDEN, "att"),
+            ("gate_up", Q4_K, 2 * FFN, HIDDEN, "hn"),
+            ("down", Q6_K, HIDDEN, FFN, "act")]
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-table", action="store_true", help="skip the per-kind matvec table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
+    ap.add_argument("--seed", type=int, default=1234)
+    return ap.parse_args()
+
+
+class Decoder:
+    """Device-resident Llama-3-8B Q4_K_M weights, in the packed layout of the
+    batch-1 kernels, and the per-token launch list."""
+
+    def __init__(self, torch, aa, synth, seed):
+        self.torch, self.dev = torch, aa.DeviceOps()
+        self.aa = aa
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+
+        def packed(kind, out, inp):
+            raw = synth.blocks_torch(kind, out * (inp // 256), generator=g)
+            p = torch.empty(self.dev.packed_bytes(kind, inp, out), dtype=torch.uint8, device="cuda")
+            self.dev.pack(kind, raw.data_ptr(), inp, out, p.data_ptr())
+            torch.cuda.synchronize()
+            return p
+
+        self.layers = [{name: packed(kind, out, inp) for name, kind, out, inp, _ in layer_plan()}
+                       for _ in range(LAYERS)]
+        self.head = packed(Q6_K, VOCAB, HIDDEN)
+        f = dict(device="cuda", dtype=torch.float32)
+        self.x = {"h": torch.randn(HIDDEN, generator=g, **f), "att": torch.randn(HIDDEN, generator=g, **f),
+                  "hn": torch.randn(HIDDEN, generator=g, **f), "act": torch.randn(FFN, generator=g, **f)}
+        self.y = {name: torch.empty(out, **f) for name, _, out, _, _ in layer_plan()}
+        self.logits = torch.empty(VOCAB, **f)
+
+    def launches(self):
+        """(kind, packed_ptr, in, out, x_key, y_ptr) per matvec, in decode order."""
+        for L in self.layers:
+            for name, kind, out, inp, xk in layer_plan():
+                yield (kind, L[name].data_ptr(), inp, out, xk, self.y[name].data_ptr())
+        yield (Q6_K, self.head.data_ptr(), HIDDEN, VOCAB, "h", self.logits.data_ptr())
+
+    def issue(self, op, stream):
+        kind, w, inp, out, xk, y = op
+        self.dev.matvec_packed(kind, w, inp, out, self.x[xk].data_ptr(), y, stream)
+
+    def step(self, stream, only=None):
+        for op in self.launches():
+            if only is None or only(op):
+                self.issue(op, stream)
+
+
+def kernel_name(aa, op):
+    return f"kq_mv_packed<{aa.KIND_NAMES[op[0]]}>"
+
+
+def op_bytes(aa, op):
+    kind, _, inp, out, _, _ = op
+    return aa.weight_bytes(kind, inp, out) + 4 * (inp + out)
+
+
+def kernel_events(torch, dec, stream, reps=5):
+    """Per kernel (kind): the step's launches of that kernel alone, captured in
+    a HIP graph and replayed `reps` times between two HIP events on the launch
+    stream; average launch duration = elapsed / launches."""
+    aa = dec.aa
+    kinds = sorted({op[0] for op in dec.launches()})
+    out = {}
+    for kind in kinds:
+        ops = [op for op in dec.launches() if op[0] == kind]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            dec.step(stream.cuda_stream, only=lambda op: op[0] == kind)
+        with torch.cuda.stream(stream):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+        stream.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = sum(op_bytes(aa, op) for op in ops)
+        out[kernel_name(aa, ops[0])] = {"launches": len(ops), "us_per_step": round(us, 1),
+                                        "avg_us": round(us / len(ops), 3), "bytes": nbytes,
+                                        "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        del g
+    return out
+
+
+def kquant_table(torch, aa, synth, seed, stream):
+    """Batch-1 matvec per K-quant at the Llama-3-8B FFN shapes (and the 4096^2
+    Q4_K q_proj), packed layout, rotating launches over >=1 GiB of distinct
+    weight copies so every launch reads cold HBM; one graph of all copies,
+    replayed."""
+    dev = aa.DeviceOps()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 1)
+    shapes = [(k, o, i) for k in (aa.Q2_K, aa.Q3_K, aa.Q4_K, aa.Q5_K, aa.Q6_K)
+              for (o, i) in ((14336, 4096), (4096, 14336))] + [(aa.Q4_K, 4096, 4096)]
+    table = {}
+    for kind, out, inp in shapes:
+        pb = dev.packed_bytes(kind, inp, out)
+        ncopy = max(8, -(-int(1.1 * GIB) // pb))
+        raw = synth.blocks_torch(kind, out * (inp // 256), generator=g)
+        P = torch.empty(ncopy * pb, dtype=torch.uint8, device="cuda")
+        dev.pack(kind, raw.data_ptr(), inp, out, P.data_ptr())
+        del raw
+        for c in range(1, ncopy):   # copies at distinct addresses: caches are address-tagged, so each launch reads HBM
+            P[c * pb:(c + 1) * pb].copy_(P[:pb])
+        x = torch.randn(inp, device="cuda", generator=g)
+        y = torch.empty(out, device="cuda")
+        with torch.cuda.stream(stream):
+            sp = stream.cuda_stream
+            dev.matvec_packed(kind, P.data_ptr(), inp, out, x.data_ptr(), y.data_ptr(), sp)
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for c in range(ncopy):
+                    dev.matvec_packed(kind, P.data_ptr() + c * pb, inp, out, x.data_ptr(), y.data_ptr(),
+                                      stream.cuda_stream)
+            graph.replay()
+            stream.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 4
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            stream.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / (reps * ncopy)
+        nbytes = aa.weight_bytes(kind, inp, out) + 4 * (inp + out)
+        gbs = nbytes / t / 1e9
+        table[f"{aa.KIND_NAMES[kind]} {out}x{inp}"] = {"us": round(t * 1e6, 2), "GBps": round(gbs, 1),
+                                                        "frac": round(gbs / HBM_PEAK_GBS, 3)}
+        print(f"# {aa.KIND_NAMES[kind]} {out}x{inp}: {t * 1e6:.2f} us {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+        del graph, P
+        torch.cuda.empty_cache()
+    return table
+
+
+def cpu_baseline(seed, threads):
+    """Aspida's CPU QMatVec (restated in C, pooled rows as LLM_Pool does) on the
+    same decode stream, timed on a bounded sample: one layer's seven matvecs
+    (139 MB of weights) and the output head, each the median of repeated runs;
+    tokens/s = 1 / (32 * layer + head)."""
+    import numpy as np
+    import oracle
+    from aspida_amd import synth
+    gen = synth.rng(seed)
+    plan = [("q", Q4_K, HIDDEN, HIDDEN), ("k", Q4_K, KV, HIDDEN), ("v", Q6_K, KV, HIDDEN),
+            ("o", Q4_K, HIDDEN, HIDDEN), ("gate", Q4_K, FFN, HIDDEN), ("up", Q4_K, FFN, HIDDEN),
+            ("down", Q6_K, HIDDEN, FFN)]
+    ws = [(kind, synth.weight_np(kind, out, inp, gen), inp, out) for _, kind, out, inp in plan]
+    head = synth.weight_np(Q6_K, VOCAB, HIDDEN, gen)
+    xs = {HIDDEN: synth.activations_np(HIDDEN, gen), FFN: synth.activations_np(FFN, gen)}
+
+    def layer():
+        for kind, w, inp, out in ws:
+            oracle.qmatvec(kind, w, inp, out, xs[inp], nthreads=threads)
+
+    def run_head():
+        oracle.qmatvec(Q6_K, head, HIDDEN, VOCAB, xs[HIDDEN], nthreads=threads)
+
+    def median_time(fn, budget_s, max_runs=60):
+        fn(); fn()                                   # two warm-up calls
+        ts, t_all = [], time.perf_counter()
+        while len(ts) < max_runs and (len(ts) < 3 or time.perf_counter() - t_all < budget_s):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts), len(ts)
+
+    t_layer, n_layer = median_time(layer, 12.0)
+    t_head, n_head = median_time(run_head, 6.0)
+    t_tok = LAYERS * t_layer + t_head
+    return {"value": round(1.0 / t_tok, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"C restatement of QMatVec (llm_dequant.adb:808-932, llm_pool.adb:91-160), "
+                       f"{threads} threads; one Llama-3-8B layer's 7 matvecs (median of {n_layer}) and the "
+                       f"Q6_K head (median of {n_head}); token = 32*layer + head = {t_tok * 1e3:.1f} ms; "
+                       f"{(LAYERS * sum(w.nbytes for _, w, _, _ in ws) + head.nbytes) / t_tok / 1e9:.2f} GB/s"),
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding is a design, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import aspida_amd as aa
+    from aspida_amd import synth
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    aa.load()                                       # fails loudly without the HIP library
+    stream = torch.cuda.Stream()
+    dec = Decoder(torch, aa, synth, args.seed)
+    torch.cuda.synchronize()
+
+    # Warm the path eagerly once (first-call set-up happens outside capture), then capture one token.
+    with torch.cuda.stream(stream):
+        dec.step(stream.cuda_stream)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        dec.step(stream.cuda_stream)
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) * 1e-3
+    tok_s = args.steps / wall
+    print(f"# decode: {args.steps} tokens in {wall * 1e3:.1f} ms wall ({gpu_s * 1e3:.1f} ms events)",
+          file=sys.stderr, flush=True)
+    del graph
+
+    # Dominant kernel: per kernel, its launches of one step in a graph of their own, timed with events.
+    groups = kernel_events(torch, dec, stream)
+    dom_key = max(groups, key=lambda k: groups[k]["us_per_step"])
+    dom = groups[dom_key]
+    achieved = dom["bytes"] / dom["launches"] / (dom["avg_us"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dom_key, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "launches_per_step": dom["launches"], "avg_launch_us": dom["avg_us"],
+                "bytes_per_launch": dom["bytes"] // dom["launches"]}
+    table = None if args.no_table else kquant_table(torch, aa, synth, args.seed, stream)
+    del dec
+    torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(args.seed, threads)
+
+    stream_bytes = 4_875_853_824
+    line = {
+        "metric": "Llama-3-8B Q4_K_M decode weight stream tok/s (batch 1) + K-quant matvec HBM GB/s",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "llama3-8b-q4_k_m-decode-weight-stream", "layers": LAYERS, "hidden": HIDDEN,
+                   "ffn": FFN, "kv_dim": KV, "vocab": VOCAB, "batch": 1,
+                   "weight_bytes_per_token": stream_bytes, "seed": args.seed},
+        "hbm_frac_of_stream": round(tok_s * stream_bytes / (HBM_PEAK_GBS * 1e9), 4),
+        "gpu_event_ms_per_step": round(gpu_s * 1e3 / args.steps, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": groups,
+        "kquant_matvec": table,
+    }
+    assert dec_bytes_ok(stream_bytes), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"
+    print(json.dumps(line), flush=True)
+
+
+def dec_bytes_ok(expected):
+    per_layer = sum({Q4_K: 144, Q6_K: 210}[k] * o * (i // 256) for _, k, o, i, _ in layer_plan())
+    return LAYERS * per_layer + 210 * VOCAB * (HIDDEN // 256) == expected
+
+
+if __name__ == "__main__":
+    main()

@@ -85,6 +85,28 @@ int aspida_kq_xsum_dev(const float *x, int in_dim, int rows, float *xq, void *st
 int aspida_kq_matvec_dev(int kind, const void *w, int in_dim, int out_dim, const float *x,
                          const float *xq, float *y, void *stream);
 
+/* Lane-interleaved ("packed") layout of the batch-1 decode kernels: tiles of
+ * 64 rows, each tile's super-block column stored as 16-byte chunk planes with
+ * one chunk per row, so a wave reads 1 KB per load and each lane owns one
+ * row.  Same bytes as the ggml layout, regrouped (rows past out_dim in the
+ * last tile are zero).  The same math as QMatVec
+ * (src/llm/llm_dequant.adb:808-932) and the reference's batch-1 kernels
+ * (gpu/gpu_matvec.cu:149-383), over a layout of this library's own.
+ * aspida_kq_packed_bytes: size of the packed image (0 for a bad kind/shape).
+ * aspida_kq_pack_dev / aspida_kq_unpack_dev: ggml <-> packed, on `stream`. */
+long long aspida_kq_packed_bytes(int kind, int in_dim, int out_dim);
+int aspida_kq_pack_dev(int kind, const void *w, int in_dim, int out_dim, void *packed, void *stream);
+int aspida_kq_unpack_dev(int kind, const void *packed, int in_dim, int out_dim, void *w, void *stream);
+
+/* y[out_dim] = W x for packed W: the batch-1 decode path.  Per-group
+ * activation sums are formed inside the kernel (no xq).  x must be 16-byte
+ * aligned.  The library keeps a small workspace per stream (allocated on the
+ * first call for a stream and shape, so warm up before graph capture);
+ * calls on one stream are ordered, calls on different streams are
+ * independent. */
+int aspida_kq_matvec_packed_dev(int kind, const void *packed, int in_dim, int out_dim, const float *x,
+                                float *y, void *stream);
+
 /* Device form of aspida_gpu_matmul; xq from aspida_kq_xsum_dev(x, .., batch). */
 int aspida_kq_matmul_dev(int kind, const void *w, int in_dim, int out_dim, int batch,
                          const float *x, const float *xq, float *y, void *stream);

@@ -2,9 +2,12 @@
 
 Dequantization is bit-exact.  Matvec outputs match the oracle's QMatVec within
 MV_RTOL (2e-5) times sum_i |w_i x_i| per output, through the reference ABI
-(aspida_gpu_matvec, host pointers) and the device-pointer entry point, over
-every kind, every launch layout, ragged row counts, one-super-block rows, the
-benchmark shapes and scale fields holding +-0, subnormals, Inf and NaN.
+(aspida_gpu_matvec, host pointers, packed HBM mirror) and the device-pointer
+entry points (packed layout, and the ggml-layout stream kernel under every
+launch-shape override), over every kind, ragged row counts, one-super-block
+rows, the benchmark shapes and scale fields holding +-0, subnormals, Inf and
+NaN.  Packing round-trips byte for byte; packed launches are deterministic
+and replay correctly from a HIP graph.
 """
 import numpy as np
 import pytest
@@ -78,22 +81,151 @@ def _check_mv(gpu, kind, out_dim, in_dim, seed, what, specials=False):
     return assert_close_scaled(y, want, scale, what=what)
 
 
-# Row lengths of 1..56 super-blocks exercise every stream shape: chunks of
-# 16/8/4/2/1 super-blocks per wave, teams of 1..7 waves, idle lanes.
+# Row lengths of 1..56 super-blocks and ragged row counts: for the packed
+# kernels every split of a tile's columns over waves and workgroups (one
+# workgroup, LDS-only, cross-workgroup partial sums), for the ggml-layout
+# stream kernel chunks of 16/8/4/2/1 super-blocks per wave, teams of 1..7
+# waves, idle lanes.
 SMALL_SHAPES = [(1, 256), (3, 512), (67, 768), (130, 4096), (257, 2304), (33, 3328), (70, 8192),
-                (41, 14336)]
+                (41, 14336), (16421, 1024)]
 CONFIGS = [(1, 16), (2, 16), (4, 16), (2, 4), (4, 64)]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_matvec_small_shapes(kind, gpu):
+    """Reference ABI (host pointers; packed HBM mirror)."""
+    for i, (out_dim, in_dim) in enumerate(SMALL_SHAPES):
+        _check_mv(gpu, kind, out_dim, in_dim, 1000 * kind + i, f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
+
+
+def _dev_mv(dev, kind, w, x, in_dim, out_dim, layout):
+    """y from the device entry points: 'stream' = ggml layout with xsum,
+    'packed' = pack then the packed matvec."""
+    torch = torch_cuda()
+    dw, dx = to_dev(w), to_dev(x)
+    dy = torch.full((out_dim,), float("nan"), dtype=torch.float32, device="cuda")
+    if layout == "stream":
+        dq = torch.empty(in_dim // 16, dtype=torch.float32, device="cuda")
+        dev.xsum(dx.data_ptr(), in_dim, 1, dq.data_ptr(), stream())
+        dev.matvec(kind, dw.data_ptr(), in_dim, out_dim, dx.data_ptr(), dq.data_ptr(), dy.data_ptr(), stream())
+    else:
+        dp = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+        dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+        dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
+    sync()
+    return dy.cpu().numpy()
+
+
+def _check_dev(dev, kind, out_dim, in_dim, seed, layout, what):
+    gen = synth.rng(seed)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    x = synth.activations_np(in_dim, gen)
+    y = _dev_mv(dev, kind, w, x, in_dim, out_dim, layout)
+    want = oracle.qmatvec(kind, w, in_dim, out_dim, x, nthreads=ncpu())
+    return assert_close_scaled(y, want, abs_dot_scale(kind, w, in_dim, out_dim, x), what=what)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_packed_matvec_small_shapes(kind, dev):
+    for i, (out_dim, in_dim) in enumerate(SMALL_SHAPES):
+        _check_dev(dev, kind, out_dim, in_dim, 3000 * kind + i, "packed", f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
 
 
 @pytest.mark.parametrize("cfg", CONFIGS, ids=lambda c: f"R{c[0]}W{c[1]}")
 @pytest.mark.parametrize("kind", KINDS)
-def test_matvec_small_shapes_all_configs(kind, cfg, gpu):
-    assert gpu.lib.aspida_kq_set_mv_config(*cfg) == 0
+def test_stream_matvec_small_shapes_all_configs(kind, cfg, dev):
+    """The ggml-layout stream kernel under every launch-shape override."""
+    assert dev.lib.aspida_kq_set_mv_config(*cfg) == 0
     try:
         for i, (out_dim, in_dim) in enumerate(SMALL_SHAPES):
-            _check_mv(gpu, kind, out_dim, in_dim, 1000 * kind + i, f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
+            _check_dev(dev, kind, out_dim, in_dim, 1000 * kind + i, "stream",
+                       f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
     finally:
-        gpu.lib.aspida_kq_set_mv_config(0, 16)
+        dev.lib.aspida_kq_set_mv_config(0, 16)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_pack_unpack_round_trip(kind, dev):
+    """Packing only moves bytes: unpack(pack(W)) == W byte for byte, the image
+    has 64-row tiles, and the rows padding the last tile are zero."""
+    torch = torch_cuda()
+    for out_dim, in_dim in [(1, 256), (64, 512), (67, 768), (200, 4096)]:
+        gen = synth.rng(50 + out_dim + kind)
+        w = gen.integers(0, 256, aa.weight_bytes(kind, in_dim, out_dim), dtype=np.uint8)
+        nb = dev.packed_bytes(kind, in_dim, out_dim)
+        assert nb == -(-out_dim // 64) * 64 * (in_dim // 256) * aa.BLOCK_BYTES[kind]
+        dw = to_dev(w)
+        dp = torch.full((nb,), 0xA5, dtype=torch.uint8, device="cuda")
+        dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+        back = torch.zeros_like(dw)
+        dev.unpack(kind, dp.data_ptr(), in_dim, out_dim, back.data_ptr(), stream())
+        sync()
+        assert np.array_equal(back.cpu().numpy(), w)
+        packed = dp.cpu().numpy()
+        assert np.count_nonzero(packed) <= w.size            # padding rows hold zeros
+        assert sorted(packed.tolist()) == sorted(np.concatenate(
+            [w, np.zeros(nb - w.size, np.uint8)]).tolist())  # a permutation of W plus zeros
+
+
+def test_packed_deterministic_and_graph_replay(dev):
+    """Cross-workgroup partial sums are added in a fixed order, so repeated
+    launches give identical bits; the launches capture into a HIP graph (the
+    arrival counters re-arm themselves, no memset) and every replay, with
+    eager work in between, reproduces the eager result."""
+    torch = torch_cuda()
+    gen = synth.rng(66)
+    shapes = [(0, 4096, 14336), (1, 1024, 4096), (0, 5120, 4096)]
+    bufs = []
+    for kind, out_dim, in_dim in shapes:
+        w = synth.weight_np(kind, out_dim, in_dim, gen)
+        x = synth.activations_np(in_dim, gen)
+        dw, dx = to_dev(w), to_dev(x)
+        dp = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+        dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+        bufs.append((kind, out_dim, in_dim, dp, dx, torch.empty(out_dim, device="cuda"), w, x))
+    s = torch.cuda.Stream()
+    sync()
+
+    def run(sp):
+        for kind, out_dim, in_dim, dp, dx, dy, _, _ in bufs:
+            dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), sp)
+
+    with torch.cuda.stream(s):
+        run(s.cuda_stream)
+    s.synchronize()
+    eager = [b[5].clone() for b in bufs]
+    with torch.cuda.stream(s):
+        run(s.cuda_stream)
+    s.synchronize()
+    for e, b in zip(eager, bufs):
+        assert torch.equal(e, b[5])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run(s.cuda_stream)
+    for rep in range(3):
+        for b in bufs:
+            b[5].fill_(float("nan"))
+        sync()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        for e, b in zip(eager, bufs):
+            assert torch.equal(e, b[5]), f"replay {rep}"
+    for (kind, out_dim, in_dim, _, _, _, w, x), e in zip(bufs, eager):
+        want = oracle.qmatvec(kind, w, in_dim, out_dim, x, nthreads=ncpu())
+        assert_close_scaled(e.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x), what="graph")
+
+
+def test_packed_rejects_bad_arguments(dev):
+    torch = torch_cuda()
+    x = torch.zeros(260, device="cuda")
+    y = torch.zeros(64, device="cuda")
+    p = torch.zeros(dev.packed_bytes(0, 256, 64), dtype=torch.uint8, device="cuda")
+    lib = dev.lib
+    assert lib.aspida_kq_matvec_packed_dev(0, p.data_ptr(), 256, 64, x.data_ptr() + 4, y.data_ptr(), None) < 0
+    assert lib.aspida_kq_matvec_packed_dev(9, p.data_ptr(), 256, 64, x.data_ptr(), y.data_ptr(), None) < 0
+    assert lib.aspida_kq_matvec_packed_dev(0, p.data_ptr(), 300, 64, x.data_ptr(), y.data_ptr(), None) < 0
+    assert lib.aspida_kq_packed_bytes(0, 300, 64) == 0
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -112,6 +244,13 @@ def test_matvec_benchmark_shapes(kind, shape, gpu):
     out_dim, in_dim = shape
     r = _check_mv(gpu, kind, out_dim, in_dim, 5 + kind, f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
     print(f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}: max |err| / sum|wx| = {r:.2e}")
+
+
+@pytest.mark.parametrize("shape", BENCH_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("kind", list(aa.KQUANTS))
+def test_stream_matvec_benchmark_shapes(kind, shape, dev):
+    out_dim, in_dim = shape
+    _check_dev(dev, kind, out_dim, in_dim, 5 + kind, "stream", f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim}")
 
 
 def test_matvec_device_entry_point(dev):

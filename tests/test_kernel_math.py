@@ -58,3 +58,50 @@ def test_aligned_loads(emul, offset):
     out[:] = 0
     emul.kq_emul_ld12e(buf.ctypes.data + base, out.ctypes.data)
     assert out[:12].tolist() == buf[base:base + 12].tolist()
+
+
+def _emul_packed(emul):
+    emul.kq_emul_packed_offset.restype = ctypes.c_int
+    emul.kq_emul_packed_offset.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    emul.kq_emul_packed_row.restype = ctypes.c_float
+    emul.kq_emul_packed_row.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    return emul
+
+
+def packed_offsets(emul, kind):
+    bb = oracle.BLOCK_BYTES[kind]
+    return np.array([[emul.kq_emul_packed_offset(kind, r, b) for b in range(bb)] for r in range(64)], np.int64)
+
+
+@pytest.mark.parametrize("kind", list(oracle.KQUANTS) + [oracle.KIND_Q8_0])
+def test_packed_layout_is_a_permutation(emul, kind):
+    """Every byte of the 64 super-blocks of a (tile, column) group has its own
+    slot, and the slots fill exactly 64 * block bytes."""
+    off = packed_offsets(_emul_packed(emul), kind)
+    assert sorted(off.ravel().tolist()) == list(range(64 * oracle.BLOCK_BYTES[kind]))
+
+
+@pytest.mark.parametrize("kind", list(oracle.KQUANTS) + [oracle.KIND_Q8_0])
+def test_packed_rows_match_oracle(emul, kind):
+    """Each lane's registers (Packed<K>::load) and quarter views
+    (Packed<K>::quarter) over a packed group reproduce the row's dot product:
+    the chunk indices agree with the ggml field offsets of every format."""
+    emul = _emul_packed(emul)
+    bb = oracle.BLOCK_BYTES[kind]
+    off = packed_offsets(emul, kind)
+    gen = synth.rng(700 + kind)
+    rows = synth.blocks_np(kind, 64, gen).reshape(64, bb)
+    rows[::7] = gen.integers(0, 256, (len(rows[::7]), bb), dtype=np.uint8)   # raw bytes too
+    buf = np.zeros(64 * bb + 32, np.uint8)
+    base = (16 - buf.ctypes.data % 16) % 16
+    grp = buf[base:base + 64 * bb]
+    grp[off.ravel()] = rows.ravel()
+    x = synth.activations_np(256, gen)
+    s16 = x.reshape(16, 16).sum(1, dtype=np.float32)
+    w = oracle.dequant(kind, rows.ravel(), 256, 64).astype(np.float64)
+    ref = w @ x.astype(np.float64)
+    scale = np.abs(w) @ np.abs(x.astype(np.float64))
+    got = np.array([emul.kq_emul_packed_row(kind, grp.ctypes.data, r, x.ctypes.data, s16.ctypes.data)
+                    for r in range(64)])
+    err = np.abs(got - ref) / np.maximum(scale, 1e-30)
+    assert err.max() < 1e-6, err.max()
