@@ -59,6 +59,7 @@ def load(path=None):
         "aspida_kq_matmul_dev": (I, [I, P, I, I, I, P, P, P, P]),
         "aspida_kq_packed_bytes": (ctypes.c_longlong, [I, I, I]),
         "aspida_kq_pack_dev": (I, [I, P, I, I, P, P]),
+        "aspida_kq_packed_plan": (I, [I, I, P, P, P]),
         "aspida_kq_unpack_dev": (I, [I, P, I, I, P, P]),
         "aspida_kq_matvec_packed_dev": (I, [I, P, I, I, P, P, P]),
         "aspida_kq_matmul_valu_dev": (I, [I, P, I, I, I, P, P, P, P]),
@@ -165,6 +166,13 @@ class DeviceOps:
 
     def packed_bytes(self, kind, in_dim, out_dim):
         return int(self.lib.aspida_kq_packed_bytes(kind, in_dim, out_dim))
+
+    def packed_plan(self, in_dim, out_dim):
+        """(waves per workgroup, workgroups per tile, columns per wave)."""
+        v = [ctypes.c_int(0) for _ in range(3)]
+        self._ok(self.lib.aspida_kq_packed_plan(in_dim, out_dim, *[ctypes.byref(a) for a in v]),
+                 "aspida_kq_packed_plan")
+        return tuple(a.value for a in v)
 
     def pack(self, kind, w, in_dim, out_dim, packed, stream=0):
         self._ok(self.lib.aspida_kq_pack_dev(kind, w, in_dim, out_dim, packed, stream), "aspida_kq_pack_dev")

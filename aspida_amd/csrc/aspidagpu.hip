@@ -437,6 +437,17 @@ extern "C" long long aspida_kq_packed_bytes(int kind, int in_dim, int out_dim) {
   return (long long)kq::packed_bytes(kind, in_dim, out_dim);
 }
 
+extern "C" int aspida_kq_packed_plan(int in_dim, int out_dim, int* waves_per_group, int* groups_per_tile,
+                                     int* columns_per_wave) {
+  if (in_dim <= 0 || in_dim % 256 || out_dim <= 0 || !waves_per_group || !groups_per_tile || !columns_per_wave)
+    return -EINVAL;
+  const kq::PackedPlan p = kq::packed_plan(in_dim, out_dim);
+  *waves_per_group = p.nw;
+  *groups_per_tile = p.ks;
+  *columns_per_wave = p.spw;
+  return 0;
+}
+
 extern "C" int aspida_kq_pack_dev(int kind, const void* w, int in_dim, int out_dim, void* packed, void* stream) {
   if (!w || !packed || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
   return check(kq::launch_pack(kind, w, in_dim, out_dim, packed, false, (hipStream_t)stream), "aspida_kq_pack_dev");

@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run one device copy of this many MiB (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
 
 
@@ -101,8 +103,10 @@ class Decoder:
                 self.issue(op, stream)
 
 
-def kernel_name(aa, op):
-    return f"kq_mv_packed<{aa.KIND_NAMES[op[0]]}>"
+def kernel_name(dec, op):
+    """The kernel symbol a launch runs: kq_mv_packed<kind, waves per workgroup>."""
+    kind, _, inp, out, _, _ = op
+    return f"kq_mv_packed<{kind}, {dec.dev.packed_plan(inp, out)[0]}>"
 
 
 def op_bytes(aa, op):
@@ -111,17 +115,17 @@ def op_bytes(aa, op):
 
 
 def kernel_events(torch, dec, stream, reps=5):
-    """Per kernel (kind): the step's launches of that kernel alone, captured in
+    """Per kernel symbol: the step's launches of that kernel alone, captured in
     a HIP graph and replayed `reps` times between two HIP events on the launch
     stream; average launch duration = elapsed / launches."""
     aa = dec.aa
-    kinds = sorted({op[0] for op in dec.launches()})
+    names = sorted({kernel_name(dec, op) for op in dec.launches()})
     out = {}
-    for kind in kinds:
-        ops = [op for op in dec.launches() if op[0] == kind]
+    for name in names:
+        ops = [op for op in dec.launches() if kernel_name(dec, op) == name]
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            dec.step(stream.cuda_stream, only=lambda op: op[0] == kind)
+            dec.step(stream.cuda_stream, only=lambda op: kernel_name(dec, op) == name)
         with torch.cuda.stream(stream):
             g.replay()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -132,11 +136,26 @@ def kernel_events(torch, dec, stream, reps=5):
         stream.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / reps
         nbytes = sum(op_bytes(aa, op) for op in ops)
-        out[kernel_name(aa, ops[0])] = {"launches": len(ops), "us_per_step": round(us, 1),
+        out[name] = {"launches": len(ops), "us_per_step": round(us, 1),
                                         "avg_us": round(us / len(ops), 3), "bytes": nbytes,
                                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
         del g
     return out
+
+
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "kq_mv_packed_llama8b_decode_traffic.json")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` in this workload, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE measurement (scaled by a copy kernel of
+    known size); None when that file has no figure for the kernel."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            k = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if k is None else k["traffic_bytes_per_launch"]
 
 
 def kquant_table(torch, aa, synth, seed, stream):
@@ -293,9 +312,16 @@ def main():
     dom = groups[dom_key]
     achieved = dom["bytes"] / dom["launches"] / (dom["avg_us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dom_key, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_key),
                 "launches_per_step": dom["launches"], "avg_launch_us": dom["avg_us"],
                 "bytes_per_launch": dom["bytes"] // dom["launches"]}
+    if args.copy_probe_mib:
+        a = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
     table = None if args.no_table else kquant_table(torch, aa, synth, args.seed, stream)
     del dec
     torch.cuda.empty_cache()

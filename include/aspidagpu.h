@@ -98,6 +98,12 @@ long long aspida_kq_packed_bytes(int kind, int in_dim, int out_dim);
 int aspida_kq_pack_dev(int kind, const void *w, int in_dim, int out_dim, void *packed, void *stream);
 int aspida_kq_unpack_dev(int kind, const void *packed, int in_dim, int out_dim, void *w, void *stream);
 
+/* Launch split aspida_kq_matvec_packed_dev uses for this shape: waves per
+ * workgroup (the kernel is kq_mv_packed<kind, waves>), workgroups per 64-row
+ * tile and super-block columns per wave (their product is in_dim / 256). */
+int aspida_kq_packed_plan(int in_dim, int out_dim, int *waves_per_group, int *groups_per_tile,
+                          int *columns_per_wave);
+
 /* y[out_dim] = W x for packed W: the batch-1 decode path.  Per-group
  * activation sums are formed inside the kernel (no xq).  x must be 16-byte
  * aligned.  The library keeps a small workspace per stream (allocated on the
