@@ -62,6 +62,7 @@ def load(path=None):
         "aspida_kq_packed_plan": (I, [I, I, P, P, P]),
         "aspida_kq_unpack_dev": (I, [I, P, I, I, P, P]),
         "aspida_kq_matvec_packed_dev": (I, [I, P, I, I, P, P, P]),
+        "aspida_kq_matmul_packed_dev": (I, [I, P, I, I, I, P, P, P]),
         "aspida_kq_matmul_valu_dev": (I, [I, P, I, I, I, P, P, P, P]),
         "aspida_kq_dequant_dev": (I, [I, P, I, I, P, P]),
         "aspida_dense_matvec_dev": (I, [P, I, I, P, P, P]),
@@ -183,6 +184,10 @@ class DeviceOps:
     def matvec_packed(self, kind, packed, in_dim, out_dim, x, y, stream=0):
         self._ok(self.lib.aspida_kq_matvec_packed_dev(kind, packed, in_dim, out_dim, x, y, stream),
                  "aspida_kq_matvec_packed_dev")
+
+    def matmul_packed(self, kind, packed, in_dim, out_dim, batch, x, y, stream=0):
+        self._ok(self.lib.aspida_kq_matmul_packed_dev(kind, packed, in_dim, out_dim, batch, x, y, stream),
+                 "aspida_kq_matmul_packed_dev")
 
     def matmul(self, kind, w, in_dim, out_dim, batch, x, xq, y, stream=0, valu=False):
         fn = self.lib.aspida_kq_matmul_valu_dev if valu else self.lib.aspida_kq_matmul_dev

@@ -161,8 +161,11 @@ struct HostBuf {
 struct MvWorkspace {
   DevBuf<float> part;
   DevBuf<unsigned> count;
-  int ensure(int in_dim, int out_dim) {
+  DevBuf<uint8_t> mm;  // activation split and partials of the MFMA product
+  int ensure(int in_dim, int out_dim, int batch = 1) {
     if (part.ensure(std::max<size_t>(kq::packed_workspace_floats(in_dim, out_dim), 64), "hipMalloc partials"))
+      return -1;
+    if (batch > 1 && mm.ensure(kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, 64)), "hipMalloc mfma"))
       return -1;
     const size_t want = kq::packed_counters(out_dim);
     if (want <= count.n) return 0;
@@ -170,6 +173,27 @@ struct MvWorkspace {
     return check(hipMemset(count.p, 0, count.n * sizeof(unsigned)), "hipMemset counters");
   }
 };
+
+// Y[batch][out] = X W^T over packed W on `st`: MFMA kernels for the kinds that
+// have them (64 activation rows per launch), else one packed matvec per row.
+hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
+                         MvWorkspace& ws, hipStream_t st) {
+  if (batch > 1 && kq::mfma_kind(kind)) {
+    for (int b0 = 0; b0 < batch; b0 += 64) {
+      const int nb = std::min(64, batch - b0);
+      const hipError_t e = kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, X + (size_t)b0 * in_dim,
+                                                         Y + (size_t)b0 * out_dim, ws.mm.p, ws.count.p, st);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  for (int b = 0; b < batch; ++b) {
+    const hipError_t e = kq::launch_matvec_packed(kind, P, in_dim, out_dim, X + (size_t)b * in_dim,
+                                                  Y + (size_t)b * out_dim, ws.part.p, ws.count.p, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
 
 // Buffers live until the process ends (thread exit does not release them).
 struct Ctx {
@@ -276,16 +300,25 @@ extern "C" void aspida_gpu_matmul(const void* w, long wbytes, int kind, int in_d
     fill_nan(y, (long)out_dim * batch);
     return;
   }
-  void* dw = weight(w, need_bytes(kind, in_dim, out_dim));
   Ctx& c = ctx();
-  int rc = dw ? 0 : -1;
-  if (!rc)
-    rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, true, [&]() {
-      hipError_t e = kq::launch_matmul_mfma(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.st);
-      if (e == hipErrorNotSupported)
-        e = kq::launch_matmul_valu(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dq.p, c.dy.p, c.st);
-      return e;
-    });
+  int rc;
+  if (batch == 1 || kq::mfma_kind(kind)) {
+    // Packed HBM mirror (shared with aspida_gpu_matvec): MFMA for Q4_K / Q6_K.
+    void* dw = packed_weight(w, kind, in_dim, out_dim);
+    rc = dw ? 0 : -1;
+    if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim, batch) ? -1 : 0;
+    if (!rc)
+      rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, false, [&]() {
+        return matmul_packed(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.ws, c.st);
+      });
+  } else {
+    void* dw = weight(w, need_bytes(kind, in_dim, out_dim));
+    rc = dw ? 0 : -1;
+    if (!rc)
+      rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, true, [&]() {
+        return kq::launch_matmul_valu(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dq.p, c.dy.p, c.st);
+      });
+  }
   if (rc) fill_nan(y, (long)out_dim * batch);
 }
 
@@ -465,19 +498,32 @@ std::mutex g_ws_mu;
 std::unordered_map<void*, MvWorkspace*> g_ws;
 }  // namespace
 
+static MvWorkspace* stream_workspace(void* stream, int in_dim, int out_dim, int batch) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  MvWorkspace*& slot = g_ws[stream];
+  if (!slot) slot = new MvWorkspace();
+  if (slot->ensure(in_dim, out_dim, batch)) return nullptr;
+  return slot;
+}
+
+extern "C" int aspida_kq_matmul_packed_dev(int kind, const void* packed, int in_dim, int out_dim, int batch,
+                                           const float* x, float* y, void* stream) {
+  if (!packed || !x || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || batch <= 0 ||
+      ((uintptr_t)x & 15))
+    return -EINVAL;
+  MvWorkspace* ws = stream_workspace(stream, in_dim, out_dim, batch);
+  if (!ws) return t_last_error ? t_last_error : -1;
+  return check(matmul_packed(kind, packed, in_dim, out_dim, batch, x, y, *ws, (hipStream_t)stream),
+               "aspida_kq_matmul_packed_dev");
+}
+
 extern "C" int aspida_kq_matvec_packed_dev(int kind, const void* packed, int in_dim, int out_dim, const float* x,
                                            float* y, void* stream) {
   if (!packed || !x || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 ||
       ((uintptr_t)x & 15))
     return -EINVAL;
-  MvWorkspace* ws;
-  {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    MvWorkspace*& slot = g_ws[stream];
-    if (!slot) slot = new MvWorkspace();
-    ws = slot;
-    if (ws->ensure(in_dim, out_dim)) return t_last_error ? t_last_error : -1;
-  }
+  MvWorkspace* ws = stream_workspace(stream, in_dim, out_dim, 1);
+  if (!ws) return t_last_error ? t_last_error : -1;
   return check(kq::launch_matvec_packed(kind, packed, in_dim, out_dim, x, y, ws->part.p, ws->count.p,
                                         (hipStream_t)stream),
                "aspida_kq_matvec_packed_dev");

@@ -50,10 +50,20 @@ PackedPlan packed_plan(int in_dim, int out_dim);
 size_t packed_bytes(int kind, int in_dim, int out_dim);
 
 // Workspace a packed matvec of this shape needs: partial sums (floats) and
-// per-tile arrival counters (unsigned, zero before the first launch; every
-// launch leaves them zero again).
+// per-tile arrival counters (unsigned, one per 256 bytes; zero before the
+// first launch, and every launch leaves them zero again).
 size_t packed_workspace_floats(int in_dim, int out_dim);
 size_t packed_counters(int out_dim);
+
+// Small-batch products on MFMA over packed W (kq_mmq.hip): kinds with an
+// MFMA kernel, workspace bytes for `batch` <= 64 activation rows, and the
+// launcher (hipErrorNotSupported for other kinds).  `count` is a per-tile
+// arrival-counter array as for launch_matvec_packed (zero before first use,
+// left zero).
+bool mfma_kind(int kind);
+size_t mfma_workspace_bytes(int in_dim, int out_dim, int batch);
+hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X,
+                                     float* Y, void* work, unsigned* count, hipStream_t s);
 
 // ggml layout -> packed (unpack = false) or back (unpack = true).
 hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void* dst, bool unpack, hipStream_t s);

@@ -26,6 +26,11 @@ namespace kq {
 
 template <int KIND> struct Packed;
 
+// Arrival counters of the cross-workgroup sums sit COUNTER_STRIDE unsigned
+// apart (256 bytes): device-scope atomics on one cache line serialize
+// (about 12 ns each on MI355X), so tiles must not share a line.
+constexpr int COUNTER_STRIDE = 64;
+
 // Offset of byte b (0..BYTES-1) of row r's super-block inside its
 // (tile, column) group, for the formats whose only irregularity is a tail.
 // Returns -1 for bytes a format maps separately.

@@ -90,18 +90,27 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restric
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(&count[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    is_last = __hip_atomic_fetch_add(&count[(size_t)tile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                       (unsigned)(ks - 1)
                   ? 1u
                   : 0u;
   __syncthreads();
   if (is_last && w == 0) {
+    // Eight partials in flight at a time, added in ascending k.
     float t = 0.f;
-    for (int k = 0; k < ks; ++k)
-      t += __hip_atomic_load(&part[((size_t)k * ntiles + tile) * 64 + lane], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    for (int k0 = 0; k0 < ks; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = k0 + u < ks ? __hip_atomic_load(&part[((size_t)(k0 + u) * ntiles + tile) * 64 + lane],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < ks) t += v[u];
+    }
     if (row < out_rows) y[row] = t;
-    if (lane == 0) __hip_atomic_store(&count[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(&count[(size_t)tile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -191,7 +200,7 @@ size_t packed_workspace_floats(int in_dim, int out_dim) {
   return p.ks > 1 ? (size_t)p.ks * ((out_dim + 63) / 64) * 64 : 0;
 }
 
-size_t packed_counters(int out_dim) { return (size_t)(out_dim + 63) / 64; }
+size_t packed_counters(int out_dim) { return (size_t)(out_dim + 63) / 64 * COUNTER_STRIDE; }
 
 template <int KIND>
 static hipError_t launch_mvp_kind(const uint8_t* P, int in_dim, int out_dim, const float* x, float* y, float* part,

@@ -209,6 +209,58 @@ def kquant_table(torch, aa, synth, seed, stream):
     return table
 
 
+def small_batch_table(torch, aa, synth, seed, stream):
+    """Small-batch products: Q4_K and Q6_K at 4096x4096 and
+    14336x4096 for B in {2, 4, 8, 16, 32, 64}, packed weights on the MFMA
+    kernels, launches rotating over >= 1 GiB of weight copies.  GB/s counts
+    W + 4 B (in + out) bytes; TFLOP/s counts 2 B in out."""
+    dev = aa.DeviceOps()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 2)
+    table = {}
+    for kind in (aa.Q4_K, aa.Q6_K):
+        for out, inp in ((4096, 4096), (14336, 4096)):
+            pb = dev.packed_bytes(kind, inp, out)
+            ncopy = max(8, -(-int(1.1 * GIB) // pb))
+            raw = synth.blocks_torch(kind, out * (inp // 256), generator=g)
+            P = torch.empty(ncopy * pb, dtype=torch.uint8, device="cuda")
+            dev.pack(kind, raw.data_ptr(), inp, out, P.data_ptr())
+            del raw
+            for c in range(1, ncopy):
+                P[c * pb:(c + 1) * pb].copy_(P[:pb])
+            for B in (2, 4, 8, 16, 32, 64):
+                X = torch.randn(B, inp, device="cuda", generator=g)
+                Y = torch.empty(B, out, device="cuda")
+                with torch.cuda.stream(stream):
+                    dev.matmul_packed(kind, P.data_ptr(), inp, out, B, X.data_ptr(), Y.data_ptr(), stream.cuda_stream)
+                    stream.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=stream):
+                        for c in range(ncopy):
+                            dev.matmul_packed(kind, P.data_ptr() + c * pb, inp, out, B, X.data_ptr(), Y.data_ptr(),
+                                              stream.cuda_stream)
+                    graph.replay()
+                    stream.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    for _ in range(3):
+                        graph.replay()
+                    e1.record(stream)
+                    stream.synchronize()
+                t = e0.elapsed_time(e1) * 1e-3 / (3 * ncopy)
+                nbytes = aa.weight_bytes(kind, inp, out) + 4 * B * (inp + out)
+                table[f"{aa.KIND_NAMES[kind]} {out}x{inp} B={B}"] = {
+                    "us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                    "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3),
+                    "TFLOPs": round(2.0 * B * inp * out / t / 1e12, 2)}
+                print(f"# {aa.KIND_NAMES[kind]} {out}x{inp} B={B}: {t * 1e6:.2f} us "
+                      f"{nbytes / t / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
+                del graph
+            del P
+            torch.cuda.empty_cache()
+    return table
+
+
 def cpu_baseline(seed, threads):
     """Aspida's CPU QMatVec (restated in C, pooled rows as LLM_Pool does) on the
     same decode stream, timed on a bounded sample: one layer's seven matvecs
@@ -323,6 +375,7 @@ def main():
         torch.cuda.synchronize()
         del a, b
     table = None if args.no_table else kquant_table(torch, aa, synth, args.seed, stream)
+    small = None if args.no_table else small_batch_table(torch, aa, synth, args.seed, stream)
     del dec
     torch.cuda.empty_cache()
 
@@ -346,6 +399,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": groups,
         "kquant_matvec": table,
+        "small_batch_mfma": small,
     }
     assert dec_bytes_ok(stream_bytes), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"
     print(json.dumps(line), flush=True)

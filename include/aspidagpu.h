@@ -113,6 +113,15 @@ int aspida_kq_packed_plan(int in_dim, int out_dim, int *waves_per_group, int *gr
 int aspida_kq_matvec_packed_dev(int kind, const void *packed, int in_dim, int out_dim, const float *x,
                                 float *y, void *stream);
 
+/* Y[batch][out_dim] = X[batch][in_dim] W^T for packed W: the small-batch
+ * path.  Q4_K and Q6_K run on MFMA (activations split into f16 hi + lo, exact
+ * integer codes, f32 scales; 64 rows per launch); other kinds run the packed
+ * matvec once per row.  x must be 16-byte aligned; workspace as for
+ * aspida_kq_matvec_packed_dev.  The same math as the reference's batched
+ * kernels (gpu/gpu_matvec.cu:234-382) without its batch limit of 32. */
+int aspida_kq_matmul_packed_dev(int kind, const void *packed, int in_dim, int out_dim, int batch,
+                                const float *x, float *y, void *stream);
+
 /* Device form of aspida_gpu_matmul; xq from aspida_kq_xsum_dev(x, .., batch). */
 int aspida_kq_matmul_dev(int kind, const void *w, int in_dim, int out_dim, int batch,
                          const float *x, const float *xq, float *y, void *stream);
