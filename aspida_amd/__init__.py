@@ -63,6 +63,7 @@ def load(path=None):
         "aspida_kq_unpack_dev": (I, [I, P, I, I, P, P]),
         "aspida_kq_matvec_packed_dev": (I, [I, P, I, I, P, P, P]),
         "aspida_kq_matmul_packed_dev": (I, [I, P, I, I, I, P, P, P]),
+        "aspida_kq_matvec2_packed_dev": (I, [I, P, I, P, I, P, I, P, I, P, P]),
         "aspida_kq_matmul_valu_dev": (I, [I, P, I, I, I, P, P, P, P]),
         "aspida_kq_dequant_dev": (I, [I, P, I, I, P, P]),
         "aspida_dense_matvec_dev": (I, [P, I, I, P, P, P]),
@@ -184,6 +185,10 @@ class DeviceOps:
     def matvec_packed(self, kind, packed, in_dim, out_dim, x, y, stream=0):
         self._ok(self.lib.aspida_kq_matvec_packed_dev(kind, packed, in_dim, out_dim, x, y, stream),
                  "aspida_kq_matvec_packed_dev")
+
+    def matvec2_packed(self, kind_a, packed_a, out_a, y_a, kind_b, packed_b, out_b, y_b, in_dim, x, stream=0):
+        self._ok(self.lib.aspida_kq_matvec2_packed_dev(kind_a, packed_a, out_a, y_a, kind_b, packed_b, out_b, y_b,
+                                                       in_dim, x, stream), "aspida_kq_matvec2_packed_dev")
 
     def matmul_packed(self, kind, packed, in_dim, out_dim, batch, x, y, stream=0):
         self._ok(self.lib.aspida_kq_matmul_packed_dev(kind, packed, in_dim, out_dim, batch, x, y, stream),

@@ -517,6 +517,26 @@ extern "C" int aspida_kq_matmul_packed_dev(int kind, const void* packed, int in_
                "aspida_kq_matmul_packed_dev");
 }
 
+extern "C" int aspida_kq_matvec2_packed_dev(int kind_a, const void* packed_a, int out_a, float* y_a, int kind_b,
+                                            const void* packed_b, int out_b, float* y_b, int in_dim, const float* x,
+                                            void* stream) {
+  if (!packed_a || !packed_b || !x || !y_a || !y_b || !valid_kind(kind_a) || !valid_kind(kind_b) || in_dim <= 0 ||
+      in_dim % 256 || out_a <= 0 || out_b <= 0 || ((uintptr_t)x & 15))
+    return -EINVAL;
+  const int rows = ((out_a + 63) / 64 + (out_b + 63) / 64) * 64;
+  MvWorkspace* ws = stream_workspace(stream, in_dim, rows, 1);
+  if (!ws) return t_last_error ? t_last_error : -1;
+  const hipStream_t st = (hipStream_t)stream;
+  if (kq::matvec2_supported(kind_a, kind_b))
+    return check(kq::launch_matvec2_packed(kind_a, packed_a, out_a, y_a, kind_b, packed_b, out_b, y_b, in_dim, x,
+                                           ws->part.p, ws->count.p, st),
+                 "aspida_kq_matvec2_packed_dev");
+  hipError_t e = kq::launch_matvec_packed(kind_a, packed_a, in_dim, out_a, x, y_a, ws->part.p, ws->count.p, st);
+  if (e == hipSuccess)
+    e = kq::launch_matvec_packed(kind_b, packed_b, in_dim, out_b, x, y_b, ws->part.p, ws->count.p, st);
+  return check(e, "aspida_kq_matvec2_packed_dev");
+}
+
 extern "C" int aspida_kq_matvec_packed_dev(int kind, const void* packed, int in_dim, int out_dim, const float* x,
                                            float* y, void* stream) {
   if (!packed || !x || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 ||

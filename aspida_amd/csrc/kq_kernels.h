@@ -55,6 +55,14 @@ size_t packed_bytes(int kind, int in_dim, int out_dim);
 size_t packed_workspace_floats(int in_dim, int out_dim);
 size_t packed_counters(int out_dim);
 
+// Two packed matrices that multiply the same x, in one launch: y_a = A x,
+// y_b = B x (workspace and counters sized for out_a + out_b rows rounded up
+// to tiles).  hipErrorNotSupported for kind pairs without a fused kernel.
+bool matvec2_supported(int kind_a, int kind_b);
+hipError_t launch_matvec2_packed(int kind_a, const void* Pa, int out_a, float* ya, int kind_b, const void* Pb,
+                                 int out_b, float* yb, int in_dim, const float* x, float* part, unsigned* count,
+                                 hipStream_t s);
+
 // Small-batch products on MFMA over packed W (kq_mmq.hip): kinds with an
 // MFMA kernel, workspace bytes for `batch` <= 64 activation rows, and the
 // launcher (hipErrorNotSupported for other kinds).  `count` is a per-tile

@@ -35,34 +35,67 @@ __device__ __forceinline__ void sb_sums(const float* __restrict__ xs, int lane, 
   for (int j = 0; j < 16; ++j) s16[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 4 * j));
 }
 
-template <int KIND, int NW>
-__global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restrict__ P, int nsb, int out_rows,
-                                                       const float* __restrict__ x, float* __restrict__ y, int spw,
-                                                       float* __restrict__ part, unsigned* __restrict__ count) {
+// One super-block column of row `lane`: sum_i w_i x_i over its 256 elements.
+template <int KIND>
+__device__ __forceinline__ float sb_dot(const typename Packed<KIND>::R& r, const float* __restrict__ xs, int lane) {
   using B = Block<KIND>;
-  using PK = Packed<KIND>;
-  constexpr int GB = 64 * B::BYTES;
+  float s16[16];
+  sb_sums(xs, lane, s16);
+  float acc = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    XQuarter X;
+    B::load_x(xs, s16, q, X);
+    acc += B::dot(Packed<KIND>::quarter(r, q), q, X);
+  }
+  return acc;
+}
+
+// Row `lane`'s dot over spw consecutive super-block columns starting at the
+// group g (activations xs).  With PF the next column's loads are issued
+// before the current column's arithmetic (twice the weight registers).
+template <int KIND, bool PF>
+__device__ __forceinline__ float columns_dot(const uint8_t* __restrict__ g, const float* __restrict__ xs, int lane,
+                                             int spw) {
+  constexpr int GB = 64 * Block<KIND>::BYTES;
+  typename Packed<KIND>::R r = Packed<KIND>::load(g, lane);
+  float acc = 0.f;
+  if (!PF) {  // one column per wave: no second register set, so more waves fit
+    for (int s = 0; s + 1 < spw; ++s) {
+      acc += sb_dot<KIND>(r, xs + (size_t)s * 256, lane);
+      r = Packed<KIND>::load(g + (size_t)(s + 1) * GB, lane);
+    }
+    return acc + sb_dot<KIND>(r, xs + (size_t)(spw - 1) * 256, lane);
+  }
+  for (int s = 0; s + 1 < spw; ++s) {
+    const typename Packed<KIND>::R nr = Packed<KIND>::load(g + (size_t)(s + 1) * GB, lane);
+    // Keep those loads issued here: without the barrier the compiler sinks
+    // them to their use in the next iteration and nothing overlaps.
+    asm volatile("" ::: "memory");
+    acc += sb_dot<KIND>(r, xs + (size_t)s * 256, lane);
+    r = nr;
+  }
+  return acc + sb_dot<KIND>(r, xs + (size_t)(spw - 1) * 256, lane);
+}
+
+// Sum of the NW waves' partial dots (LDS) and of the tile's ks = gridDim.y
+// workgroups (workspace), then y.  `gtile` indexes the workspace and
+// counters (tiles of every segment of a launch), `tile` the rows of y.
+//
+// Cross-workgroup sum: the partials and the counter are device-scope (sc1)
+// atomics, which bypass the per-XCD L2s, so no agent-scope fence -- an L2
+// write-back and invalidate on this chip -- is needed: the wait below retires
+// the partial store before the arrival is counted, and the last arrival reads
+// the partials only after its counter update returned, adding them in
+// ascending order.
+template <int NW>
+__device__ __forceinline__ void mv_epilogue(float acc, int gtile, int tile, int out_rows, float* __restrict__ y,
+                                            float* __restrict__ part, unsigned* __restrict__ count) {
   __shared__ float red[NW > 1 ? NW * 64 : 1];
   __shared__ unsigned is_last;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = blockIdx.x;
   const int ks = gridDim.y;
-  const int sb0 = (blockIdx.y * NW + w) * spw;
-  const uint8_t* g = P + ((size_t)tile * nsb + sb0) * GB;
-  const float* xs = x + (size_t)sb0 * 256;
-  float acc = 0.f;
-  for (int s = 0; s < spw; ++s, g += GB, xs += 256) {
-    const typename PK::R r = PK::load(g, lane);
-    float s16[16];
-    sb_sums(xs, lane, s16);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      XQuarter X;
-      B::load_x(xs, s16, q, X);
-      acc += B::dot(PK::quarter(r, q), q, X);
-    }
-  }
   if (NW > 1) {
     red[w * 64 + lane] = acc;
     __syncthreads();
@@ -78,20 +111,15 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restric
     if (w == 0 && row < out_rows) y[row] = acc;
     return;
   }
-  // Cross-workgroup sum.  The partials and the counter are device-scope
-  // (sc1) atomics, which bypass the per-XCD L2s, so no agent-scope fence --
-  // an L2 write-back and invalidate on this chip -- is needed: the wait
-  // below retires the partial store before the arrival is counted, and the
-  // last arrival reads the partials only after its counter update returned.
   const size_t ntiles = gridDim.x;
   if (w == 0)
-    __hip_atomic_store(&part[((size_t)blockIdx.y * ntiles + tile) * 64 + lane], acc, __ATOMIC_RELAXED,
+    __hip_atomic_store(&part[((size_t)blockIdx.y * ntiles + gtile) * 64 + lane], acc, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(&count[(size_t)tile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                      (unsigned)(ks - 1)
+    is_last = __hip_atomic_fetch_add(&count[(size_t)gtile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks - 1)
                   ? 1u
                   : 0u;
   __syncthreads();
@@ -102,7 +130,7 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restric
       float v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        v[u] = k0 + u < ks ? __hip_atomic_load(&part[((size_t)(k0 + u) * ntiles + tile) * 64 + lane],
+        v[u] = k0 + u < ks ? __hip_atomic_load(&part[((size_t)(k0 + u) * ntiles + gtile) * 64 + lane],
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                            : 0.f;
 #pragma unroll
@@ -110,7 +138,44 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restric
         if (k0 + u < ks) t += v[u];
     }
     if (row < out_rows) y[row] = t;
-    if (lane == 0) __hip_atomic_store(&count[(size_t)tile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0)
+      __hip_atomic_store(&count[(size_t)gtile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <int KIND, int NW, bool PF>
+__global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restrict__ P, int nsb, int out_rows,
+                                                       const float* __restrict__ x, float* __restrict__ y, int spw,
+                                                       float* __restrict__ part, unsigned* __restrict__ count) {
+  constexpr int GB = 64 * Block<KIND>::BYTES;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x;
+  const int sb0 = (blockIdx.y * NW + w) * spw;
+  const float acc = columns_dot<KIND, PF>(P + ((size_t)tile * nsb + sb0) * GB, x + (size_t)sb0 * 256, lane, spw);
+  mv_epilogue<NW>(acc, tile, tile, out_rows, y, part, count);
+}
+
+// Two matrices that multiply the same x in one launch: tiles [0, tiles_a) of
+// the grid are matrix A's (kind KA), the rest matrix B's (kind KB).  Both use
+// the launch's column split.
+template <int KA, int KB, int NW, bool PF>
+__global__ __launch_bounds__(64 * NW) void kq_mv_packed2(const uint8_t* __restrict__ Pa, int out_a, float* __restrict__ ya,
+                                                        const uint8_t* __restrict__ Pb, int out_b, float* __restrict__ yb,
+                                                        int tiles_a, int nsb, const float* __restrict__ x, int spw,
+                                                        float* __restrict__ part, unsigned* __restrict__ count) {
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gtile = blockIdx.x;
+  const int sb0 = (blockIdx.y * NW + w) * spw;
+  const float* xs = x + (size_t)sb0 * 256;
+  if (gtile < tiles_a) {
+    const float acc = columns_dot<KA, PF>(Pa + ((size_t)gtile * nsb + sb0) * (64 * Block<KA>::BYTES), xs, lane, spw);
+    mv_epilogue<NW>(acc, gtile, gtile, out_a, ya, part, count);
+  } else {
+    const int tile = gtile - tiles_a;
+    const float acc = columns_dot<KB, PF>(Pb + ((size_t)tile * nsb + sb0) * (64 * Block<KB>::BYTES), xs, lane, spw);
+    mv_epilogue<NW>(acc, gtile, tile, out_b, yb, part, count);
   }
 }
 
@@ -209,8 +274,15 @@ static hipError_t launch_mvp_kind(const uint8_t* P, int in_dim, int out_dim, con
   const dim3 grid((out_dim + 63) / 64, p.ks);
   const int nsb = in_dim / 256;
   switch (p.nw) {
-#define KQ_MVP(N) \
-  case N: hipLaunchKernelGGL((kq_mv_packed<KIND, N>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw, part, count); break;
+#define KQ_MVP(N)                                                                                              \
+  case N:                                                                                                      \
+    if (p.spw > 1)                                                                                             \
+      hipLaunchKernelGGL((kq_mv_packed<KIND, N, true>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw, \
+                         part, count);                                                                         \
+    else                                                                                                       \
+      hipLaunchKernelGGL((kq_mv_packed<KIND, N, false>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw, \
+                         part, count);                                                                         \
+    break;
     KQ_MVP(16) KQ_MVP(8) KQ_MVP(4) KQ_MVP(2) KQ_MVP(1)
 #undef KQ_MVP
     default: return hipErrorInvalidValue;
@@ -230,6 +302,53 @@ hipError_t launch_matvec_packed(int kind, const void* P, int in_dim, int out_dim
     case Q8_0: return launch_mvp_kind<Q8_0>(w, in_dim, out_dim, x, y, part, count, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Kind pairs with a fused two-matrix kernel (the attention input projections
+// of the common quantization mixes).
+#define KQ_PAIRS(X) X(Q4_K, Q6_K) X(Q5_K, Q6_K) X(Q4_K, Q4_K) X(Q6_K, Q6_K) X(Q5_K, Q5_K) X(Q8_0, Q8_0)
+
+bool matvec2_supported(int kind_a, int kind_b) {
+#define KQ_PAIR_OK(A, B) if (kind_a == A && kind_b == B) return true;
+  KQ_PAIRS(KQ_PAIR_OK)
+#undef KQ_PAIR_OK
+  return false;
+}
+
+template <int KA, int KB>
+static hipError_t launch_mv2_pair(const void* Pa, int out_a, float* ya, const void* Pb, int out_b, float* yb,
+                                  int in_dim, const float* x, float* part, unsigned* count, hipStream_t s) {
+  const int tiles_a = (out_a + 63) / 64, tiles_b = (out_b + 63) / 64;
+  const PackedPlan p = packed_plan(in_dim, (tiles_a + tiles_b) * 64);
+  const dim3 grid(tiles_a + tiles_b, p.ks);
+  const int nsb = in_dim / 256;
+  const uint8_t* a = (const uint8_t*)Pa;
+  const uint8_t* b = (const uint8_t*)Pb;
+  switch (p.nw) {
+#define KQ_MV2(N)                                                                                             \
+  case N:                                                                                                     \
+    if (p.spw > 1)                                                                                            \
+      hipLaunchKernelGGL((kq_mv_packed2<KA, KB, N, true>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb, \
+                         tiles_a, nsb, x, p.spw, part, count);                                                \
+    else                                                                                                      \
+      hipLaunchKernelGGL((kq_mv_packed2<KA, KB, N, false>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb, \
+                         tiles_a, nsb, x, p.spw, part, count);                                                \
+    break;
+    KQ_MV2(16) KQ_MV2(8) KQ_MV2(4) KQ_MV2(2) KQ_MV2(1)
+#undef KQ_MV2
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_matvec2_packed(int kind_a, const void* Pa, int out_a, float* ya, int kind_b, const void* Pb,
+                                 int out_b, float* yb, int in_dim, const float* x, float* part, unsigned* count,
+                                 hipStream_t s) {
+#define KQ_PAIR_GO(A, B) \
+  if (kind_a == A && kind_b == B) return launch_mv2_pair<A, B>(Pa, out_a, ya, Pb, out_b, yb, in_dim, x, part, count, s);
+  KQ_PAIRS(KQ_PAIR_GO)
+#undef KQ_PAIR_GO
+  return hipErrorNotSupported;
 }
 
 hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void* dst, bool unpack, hipStream_t s) {

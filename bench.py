@@ -38,12 +38,16 @@ Q4_K, Q6_K = 0, 1
 
 
 def layer_plan():
-    """(name, kind, out_dim, in_dim, input) per matvec launch of one layer."""
+    """(name, kind, out_dim, in_dim, input) per weight matrix of one layer."""
     return [("qk", Q4_K, HIDDEN + KV, HIDDEN, "h"),
             ("v", Q6_K, KV, HIDDEN, "h"),
             ("o", Q4_K, HIDDEN, HIDDEN, "att"),
             ("gate_up", Q4_K, 2 * FFN, HIDDEN, "hn"),
             ("down", Q6_K, HIDDEN, FFN, "act")]
+
+
+# Launches of one layer: q|k and v share their input and run as one launch.
+LAYER_LAUNCHES = [("qk", "v"), ("o",), ("gate_up",), ("down",)]
 
 
 def parse():
@@ -87,15 +91,22 @@ class Decoder:
         self.logits = torch.empty(VOCAB, **f)
 
     def launches(self):
-        """(kind, packed_ptr, in, out, x_key, y_ptr) per matvec, in decode order."""
+        """Per launch, in decode order: a tuple of (kind, packed_ptr, in, out, x_key, y_ptr), one entry per
+        matrix of the launch."""
+        plan = {name: (kind, out, inp, xk) for name, kind, out, inp, xk in layer_plan()}
         for L in self.layers:
-            for name, kind, out, inp, xk in layer_plan():
-                yield (kind, L[name].data_ptr(), inp, out, xk, self.y[name].data_ptr())
-        yield (Q6_K, self.head.data_ptr(), HIDDEN, VOCAB, "h", self.logits.data_ptr())
+            for names in LAYER_LAUNCHES:
+                yield tuple((plan[n][0], L[n].data_ptr(), plan[n][2], plan[n][1], plan[n][3], self.y[n].data_ptr())
+                            for n in names)
+        yield ((Q6_K, self.head.data_ptr(), HIDDEN, VOCAB, "h", self.logits.data_ptr()),)
 
     def issue(self, op, stream):
-        kind, w, inp, out, xk, y = op
-        self.dev.matvec_packed(kind, w, inp, out, self.x[xk].data_ptr(), y, stream)
+        if len(op) == 1:
+            kind, w, inp, out, xk, y = op[0]
+            self.dev.matvec_packed(kind, w, inp, out, self.x[xk].data_ptr(), y, stream)
+        else:
+            (ka, wa, inp, oa, xk, ya), (kb, wb, _, ob, _, yb) = op
+            self.dev.matvec2_packed(ka, wa, oa, ya, kb, wb, ob, yb, inp, self.x[xk].data_ptr(), stream)
 
     def step(self, stream, only=None):
         for op in self.launches():
@@ -104,14 +115,19 @@ class Decoder:
 
 
 def kernel_name(dec, op):
-    """The kernel symbol a launch runs: kq_mv_packed<kind, waves per workgroup>."""
-    kind, _, inp, out, _, _ = op
-    return f"kq_mv_packed<{kind}, {dec.dev.packed_plan(inp, out)[0]}>"
+    """The kernel symbol a launch runs: kq_mv_packed<kind, waves, prefetch> or
+    kq_mv_packed2<kind_a, kind_b, waves, prefetch> (the launch split is the
+    library's, aspida_kq_packed_plan)."""
+    rows = sum(-(-o // 64) * 64 for _, _, _, o, _, _ in op)
+    nw, _, spw = dec.dev.packed_plan(op[0][2], rows)
+    pf = "true" if spw > 1 else "false"
+    kinds = ", ".join(str(m[0]) for m in op)
+    return f"kq_mv_packed{'2' if len(op) > 1 else ''}<{kinds}, {nw}, {pf}>"
 
 
 def op_bytes(aa, op):
-    kind, _, inp, out, _, _ = op
-    return aa.weight_bytes(kind, inp, out) + 4 * (inp + out)
+    inp = op[0][2]
+    return sum(aa.weight_bytes(kind, inp, out) + 4 * out for kind, _, _, out, _, _ in op) + 4 * inp
 
 
 def kernel_events(torch, dec, stream, reps=5):

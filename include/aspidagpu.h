@@ -113,6 +113,15 @@ int aspida_kq_packed_plan(int in_dim, int out_dim, int *waves_per_group, int *gr
 int aspida_kq_matvec_packed_dev(int kind, const void *packed, int in_dim, int out_dim, const float *x,
                                 float *y, void *stream);
 
+/* y_a = A x and y_b = B x for two packed matrices that share the input (e.g.
+ * the q|k and v projections of a decoder layer), in one launch for the kind
+ * pairs (Q4_K, Q6_K), (Q5_K, Q6_K) and equal kinds Q4_K, Q5_K, Q6_K, Q8_0;
+ * other pairs run as two launches.  Same results as two calls of
+ * aspida_kq_matvec_packed_dev. */
+int aspida_kq_matvec2_packed_dev(int kind_a, const void *packed_a, int out_a, float *y_a, int kind_b,
+                                 const void *packed_b, int out_b, float *y_b, int in_dim, const float *x,
+                                 void *stream);
+
 /* Y[batch][out_dim] = X[batch][in_dim] W^T for packed W: the small-batch
  * path.  Q4_K and Q6_K run on MFMA (activations split into f16 hi + lo, exact
  * integer codes, f32 scales; 64 rows per launch); other kinds run the packed

@@ -216,6 +216,34 @@ def test_packed_deterministic_and_graph_replay(dev):
         assert_close_scaled(e.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x), what="graph")
 
 
+PAIR_CASES = [(aa.Q4_K, 5120, aa.Q6_K, 1024, 4096), (aa.Q5_K, 70, aa.Q6_K, 200, 2048), (aa.Q4_K, 64, aa.Q4_K, 3, 768),
+              (aa.Q8_0, 130, aa.Q8_0, 64, 1024), (aa.Q6_K, 17, aa.Q6_K, 33, 14336), (aa.Q3_K, 40, aa.Q2_K, 50, 512)]
+
+
+@pytest.mark.parametrize("case", PAIR_CASES, ids=lambda c: f"{aa.KIND_NAMES[c[0]]}{c[1]}_{aa.KIND_NAMES[c[2]]}{c[3]}_{c[4]}")
+def test_packed_matvec_pair(case, dev):
+    """Two matrices sharing x in one launch (last case: a pair without a fused
+    kernel, served as two launches) equal the oracle for both outputs."""
+    torch = torch_cuda()
+    ka, oa, kb, ob, in_dim = case
+    gen = synth.rng(4000 + oa + ob)
+    wa, wb = synth.weight_np(ka, oa, in_dim, gen), synth.weight_np(kb, ob, in_dim, gen)
+    x = synth.activations_np(in_dim, gen)
+    pa = torch.empty(dev.packed_bytes(ka, in_dim, oa), dtype=torch.uint8, device="cuda")
+    pb = torch.empty(dev.packed_bytes(kb, in_dim, ob), dtype=torch.uint8, device="cuda")
+    dev.pack(ka, to_dev(wa).data_ptr(), in_dim, oa, pa.data_ptr(), stream())
+    dev.pack(kb, to_dev(wb).data_ptr(), in_dim, ob, pb.data_ptr(), stream())
+    dx = to_dev(x)
+    ya = torch.full((oa,), float("nan"), device="cuda")
+    yb = torch.full((ob,), float("nan"), device="cuda")
+    dev.matvec2_packed(ka, pa.data_ptr(), oa, ya.data_ptr(), kb, pb.data_ptr(), ob, yb.data_ptr(), in_dim,
+                       dx.data_ptr(), stream())
+    sync()
+    for k, w, o, y in ((ka, wa, oa, ya), (kb, wb, ob, yb)):
+        want = oracle.qmatvec(k, w, in_dim, o, x, nthreads=ncpu())
+        assert_close_scaled(y.cpu().numpy(), want, abs_dot_scale(k, w, in_dim, o, x), what=aa.KIND_NAMES[k])
+
+
 def test_packed_rejects_bad_arguments(dev):
     torch = torch_cuda()
     x = torch.zeros(260, device="cuda")
