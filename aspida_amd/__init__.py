@@ -70,6 +70,9 @@ def load(path=None):
         "aspida_moe_route_dev": (I, [P, I, I, I, I, P, P, P, P, P]),
         "aspida_moe_work_floats": (LG, [I, I, I, I]),
         "aspida_moe_experts_dev": (I, [P, I, I, I, I, I, P, P] + [P, LG, I] * 3 + [P, I] * 3 + [P, P, P, P]),
+        "aspida_moe_packed_work_bytes": (LG, [I, I, I, I]),
+        "aspida_moe_pack_experts_dev": (I, [I, P, LG, I, I, I, P, P]),
+        "aspida_moe_experts_packed_dev": (I, [P, I, I, I, I, I, P, P, P, P, I, P, I, P, P, P, P, P, P, P]),
         "aspida_kq_set_mv_config": (I, [I, I]),
     }
     for name, (res, args) in sig.items():
@@ -218,6 +221,25 @@ class DeviceOps:
         self._ok(self.lib.aspida_moe_experts_dev(x, T, dim, top_k, intermed, n_exp, top_idx, top_w, *args,
                                                  shared_gate_inp or 0, work, y, stream),
                  "aspida_moe_experts_dev")
+
+    def moe_packed_work_bytes(self, T, dim, intermed, top_k):
+        n = int(self.lib.aspida_moe_packed_work_bytes(T, dim, intermed, top_k))
+        if n < 0:
+            raise ValueError(f"aspida_moe_packed_work_bytes: bad arguments ({T}, {dim}, {intermed}, {top_k})")
+        return n
+
+    def pack_experts(self, kind, src, src_stride, in_dim, out_dim, n, dst, stream=0):
+        """Pack n ggml matrices src_stride bytes apart into dst, packed_bytes apart."""
+        self._ok(self.lib.aspida_moe_pack_experts_dev(kind, src, src_stride, in_dim, out_dim, n, dst, stream),
+                 "aspida_moe_pack_experts_dev")
+
+    def moe_experts_packed(self, x, T, dim, top_k, intermed, n_exp, top_idx, top_w, gate, up, gu_kind, down,
+                           down_kind, shg, shu, shd, shared_gate_inp, work, y, stream=0):
+        """Grouped MoE experts over packed expert tensors (device pointers)."""
+        self._ok(self.lib.aspida_moe_experts_packed_dev(x, T, dim, top_k, intermed, n_exp, top_idx, top_w, gate, up,
+                                                        gu_kind, down, down_kind, shg, shu, shd,
+                                                        shared_gate_inp or 0, work, y, stream),
+                 "aspida_moe_experts_packed_dev")
 
     def set_mv_config(self, rows_per_wave=0, waves_per_cu=16):
         self._ok(self.lib.aspida_kq_set_mv_config(rows_per_wave, waves_per_cu), "aspida_kq_set_mv_config")

@@ -89,37 +89,44 @@ void* weight(const void* w, long bytes) {
 }
 
 // Device mirror of the matrix at w in the lane-interleaved layout of the
-// batch-1 kernels, packed on the device from a temporary ggml copy.  Keyed by
-// host pointer; a different kind or shape for the same pointer re-packs.
+// batch-1 kernels, packed on the device from a temporary ggml copy.  For n > 1
+// the host holds n matrices src_stride bytes apart (MoE experts) and the
+// mirror holds them packed_bytes apart.  Keyed by host pointer; a different
+// kind, shape or count for the same pointer re-packs.
 struct PEnt {
   void* d;
-  int kind, in_dim, out_dim;
+  int kind, in_dim, out_dim, n;
 };
 std::unordered_map<const void*, PEnt> g_pcache;
 
-void* packed_weight(const void* w, int kind, int in_dim, int out_dim) {
+void* packed_weight(const void* w, int kind, int in_dim, int out_dim, int n = 1, size_t src_stride = 0) {
   std::lock_guard<std::mutex> lk(g_wmu);
   auto it = g_pcache.find(w);
   if (it != g_pcache.end()) {
     const PEnt& e = it->second;
-    if (e.kind == kind && e.in_dim == in_dim && e.out_dim == out_dim) return e.d;
+    if (e.kind == kind && e.in_dim == in_dim && e.out_dim == out_dim && e.n == n) return e.d;
     (void)hipFree(e.d);
     g_pcache.erase(it);
   }
-  const size_t raw = (size_t)need_bytes(kind, in_dim, out_dim);
+  const size_t one = (size_t)need_bytes(kind, in_dim, out_dim);
+  if (n == 1) src_stride = one;
+  const size_t raw = src_stride * (size_t)(n - 1) + one;
   const size_t pb = kq::packed_bytes(kind, in_dim, out_dim);
   void *tmp = nullptr, *d = nullptr;
   int rc = check(hipMalloc(&tmp, raw), "weight upload: hipMalloc");
-  if (!rc) rc = check(hipMalloc(&d, pb), "weight upload: hipMalloc packed");
+  if (!rc) rc = check(hipMalloc(&d, pb * (size_t)n), "weight upload: hipMalloc packed");
   if (!rc) rc = check(hipMemcpy(tmp, w, raw, hipMemcpyHostToDevice), "weight upload: hipMemcpy");
-  if (!rc) rc = check(kq::launch_pack(kind, tmp, in_dim, out_dim, d, false, nullptr), "weight upload: pack");
+  for (int i = 0; i < n && !rc; ++i)
+    rc = check(kq::launch_pack(kind, (const uint8_t*)tmp + src_stride * i, in_dim, out_dim, (uint8_t*)d + pb * i,
+                               false, nullptr),
+               "weight upload: pack");
   if (!rc) rc = check(hipStreamSynchronize(nullptr), "weight upload: sync");
   if (tmp) (void)hipFree(tmp);
   if (rc) {
     if (d) (void)hipFree(d);
     return nullptr;
   }
-  g_pcache[w] = {d, kind, in_dim, out_dim};
+  g_pcache[w] = {d, kind, in_dim, out_dim, n};
   return d;
 }
 
@@ -394,6 +401,54 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
     fill_nan(y, dim);
     return;
   }
+  Ctx& c = ctx();
+  const bool gated = gate_inp_len > 1 && shared_gate_inp;
+  // Grouped path over packed experts when gate, up and the shared gate/up
+  // share one kind and both downs another (the Q4_K_M layouts do).
+  if (gate_kind == up_kind && shg_kind == gate_kind && shu_kind == gate_kind && shd_kind == down_kind &&
+      kq::moe_grouped_supported(dim, intermed, 1, top_k)) {
+    kq::MoeGroupedArgs a{};
+    // The per-expert stride of the host tensors is bytes / n_exp (gpu_matvec.cu:1702-1703).
+    a.gate = (const uint8_t*)packed_weight(gate_w, gate_kind, dim, intermed, n_exp, (size_t)(gate_bytes / n_exp));
+    a.up = (const uint8_t*)packed_weight(up_w, up_kind, dim, intermed, n_exp, (size_t)(up_bytes / n_exp));
+    a.down = (const uint8_t*)packed_weight(down_w, down_kind, intermed, dim, n_exp, (size_t)(down_bytes / n_exp));
+    a.sh_gate = (const uint8_t*)packed_weight(shg_w, shg_kind, dim, intermed);
+    a.sh_up = (const uint8_t*)packed_weight(shu_w, shu_kind, dim, intermed);
+    a.sh_down = (const uint8_t*)packed_weight(shd_w, shd_kind, intermed, dim);
+    a.gu_stride = kq::packed_bytes(gate_kind, dim, intermed);
+    a.d_stride = kq::packed_bytes(down_kind, intermed, dim);
+    a.T = 1; a.top_k = top_k; a.n_exp = n_exp; a.dim = dim; a.I = intermed;
+    int rc = (a.gate && a.up && a.down && a.sh_gate && a.sh_up && a.sh_down) ? 0 : -1;
+    if (!rc && gated) {
+      a.sgi = (const float*)weight(shared_gate_inp, (long)dim * 4);
+      if (!a.sgi) rc = -1;
+    }
+    // Staging x | top_w | top_idx, then the grouped work on a 256-byte boundary.
+    const size_t stage = ((size_t)dim + 2 * top_k + 63) & ~(size_t)63;
+    const size_t scratch = stage + (kq::moe_grouped_work_bytes(1, dim, intermed, top_k) + 3) / 4;
+    if (!rc && (c.init() || c.dy.ensure((size_t)dim, "hipMalloc y") || c.dh.ensure(scratch, "hipMalloc moe scratch") ||
+                c.hx.ensure((size_t)dim + 2 * top_k, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
+      rc = -1;
+    if (!rc) {
+      std::memcpy(c.hx.p, x, (size_t)dim * 4);
+      std::memcpy(c.hx.p + dim, top_w, (size_t)top_k * 4);
+      std::memcpy(c.hx.p + dim + top_k, top_idx, (size_t)top_k * 4);
+      rc = check(hipMemcpyAsync(c.dh.p, c.hx.p, ((size_t)dim + 2 * top_k) * 4, hipMemcpyHostToDevice, c.st), "H2D");
+      if (!rc) {
+        a.x = c.dh.p;
+        a.top_w = c.dh.p + dim;
+        a.idx = (const int*)(c.dh.p + dim + top_k);
+        a.y = c.dy.p;
+        kq::moe_grouped_bind(a, c.dh.p + stage);
+        rc = check(kq::launch_moe_grouped(a, gate_kind, down_kind, c.st), "moe launch");
+      }
+      if (!rc) rc = check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)dim * 4, hipMemcpyDeviceToHost, c.st), "D2H");
+      if (!rc) rc = check(hipStreamSynchronize(c.st), "sync");
+      if (!rc) std::memcpy(y, c.hy.p, (size_t)dim * 4);
+    }
+    if (rc) fill_nan(y, dim);
+    return;
+  }
   kq::MoeWeights mw;
   // The per-expert stride is bytes / n_exp (gpu_matvec.cu:1702-1703).
   mw.gate = (const uint8_t*)weight(gate_w, gate_bytes);
@@ -408,9 +463,7 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
   mw.gate_kind = gate_kind; mw.up_kind = up_kind; mw.down_kind = down_kind;
   mw.sh_gate_kind = shg_kind; mw.sh_up_kind = shu_kind; mw.sh_down_kind = shd_kind;
   mw.dim = dim; mw.intermed = intermed; mw.n_exp = n_exp;
-  Ctx& c = ctx();
   int rc = (mw.gate && mw.up && mw.down && mw.sh_gate && mw.sh_up && mw.sh_down) ? 0 : -1;
-  const bool gated = gate_inp_len > 1 && shared_gate_inp;
   const float* dsgi = nullptr;
   if (!rc && gated) {
     dsgi = (const float*)weight(shared_gate_inp, (long)dim * 4);
@@ -619,6 +672,61 @@ extern "C" int aspida_moe_experts_dev(const float* x, int T, int dim, int top_k,
   return check(kq::launch_moe_experts(mw, T, top_k, x, top_idx, top_w, shared_gate_inp, wk, y,
                                       (hipStream_t)stream),
                "aspida_moe_experts_dev");
+}
+
+// Tokens per grouped launch: every expert lists at most MOE_MAX_JOBS jobs.
+static int moe_chunk(int T, int top_k) { return std::min(T, kq::MOE_MAX_JOBS / top_k); }
+
+extern "C" long aspida_moe_packed_work_bytes(int T, int dim, int intermed, int top_k) {
+  if (T <= 0 || dim <= 0 || intermed <= 0 || top_k <= 0 || top_k > kq::MOE_MAX_TOPK) return -EINVAL;
+  return (long)kq::moe_grouped_work_bytes(moe_chunk(T, top_k), dim, intermed, top_k);
+}
+
+extern "C" int aspida_moe_pack_experts_dev(int kind, const void* src, long src_stride, int in_dim, int out_dim,
+                                           int n, void* dst, void* stream) {
+  if (!src || !dst || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || n <= 0 ||
+      src_stride < need_bytes(kind, in_dim, out_dim))
+    return -EINVAL;
+  const size_t pb = kq::packed_bytes(kind, in_dim, out_dim);
+  for (int i = 0; i < n; ++i) {
+    const int rc = check(kq::launch_pack(kind, (const uint8_t*)src + (size_t)src_stride * i, in_dim, out_dim,
+                                         (uint8_t*)dst + pb * i, false, (hipStream_t)stream),
+                         "aspida_moe_pack_experts_dev");
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int top_k, int intermed, int n_exp,
+                                             const int* top_idx, const float* top_w, const void* gate_p,
+                                             const void* up_p, int gu_kind, const void* down_p, int down_kind,
+                                             const void* shg_p, const void* shu_p, const void* shd_p,
+                                             const float* shared_gate_inp, void* work, float* y, void* stream) {
+  const bool ok = x && top_idx && top_w && gate_p && up_p && down_p && shg_p && shu_p && shd_p && work && y &&
+                  valid_kind(gu_kind) && valid_kind(down_kind) && T > 0 && n_exp > 0 && top_k > 0 &&
+                  top_k <= n_exp && kq::moe_grouped_supported(dim, intermed, 1, top_k) &&
+                  ((uintptr_t)x & 15) == 0 && ((uintptr_t)work & 255) == 0;
+  if (!ok) return -EINVAL;
+  kq::MoeGroupedArgs a{};
+  a.gate = (const uint8_t*)gate_p; a.up = (const uint8_t*)up_p; a.down = (const uint8_t*)down_p;
+  a.sh_gate = (const uint8_t*)shg_p; a.sh_up = (const uint8_t*)shu_p; a.sh_down = (const uint8_t*)shd_p;
+  a.gu_stride = kq::packed_bytes(gu_kind, dim, intermed);
+  a.d_stride = kq::packed_bytes(down_kind, intermed, dim);
+  a.sgi = shared_gate_inp;
+  a.top_k = top_k; a.n_exp = n_exp; a.dim = dim; a.I = intermed;
+  const int chunk = moe_chunk(T, top_k);
+  for (int t0 = 0; t0 < T; t0 += chunk) {
+    a.T = std::min(chunk, T - t0);
+    a.x = x + (size_t)t0 * dim;
+    a.idx = top_idx + (size_t)t0 * top_k;
+    a.top_w = top_w + (size_t)t0 * top_k;
+    a.y = y + (size_t)t0 * dim;
+    kq::moe_grouped_bind(a, work);
+    const int rc = check(kq::launch_moe_grouped(a, gu_kind, down_kind, (hipStream_t)stream),
+                         "aspida_moe_experts_packed_dev");
+    if (rc) return rc;
+  }
+  return 0;
 }
 
 extern "C" int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu) {

@@ -37,6 +37,37 @@ hipError_t launch_moe_experts(const MoeWeights& w, int T, int top_k, const float
                               const float* top_w, const float* shared_gate_inp, float* work, float* y,
                               hipStream_t s);
 
+// ---- grouped path over packed expert weights (kq_moe_grouped.hip) ----
+
+// Jobs (token, slot) one expert can serve per launch (T * top_k bound).
+constexpr int MOE_MAX_JOBS = 1024;
+
+// Packed expert tensors: expert e's matrix at base + e * stride (stride =
+// packed bytes of one [rows][cols] matrix); the shared expert's matrices
+// separately, same kinds.  Work arrays are device memory the caller owns
+// (moe_grouped_work_bytes).
+struct MoeGroupedArgs {
+  const uint8_t *gate, *up, *down, *sh_gate, *sh_up, *sh_down;
+  size_t gu_stride, d_stride;
+  const int* idx;        // [T][top_k] expert ids (0-based)
+  const float* top_w;    // [T][top_k]
+  const float* x;        // [T][dim], 16-byte aligned rows
+  const float* sgi;      // shared gate input [dim] or null
+  float *h, *yk, *gsh, *y;
+  unsigned* count;       // [T][tiles_dim] arrival counters, one per 256 bytes
+  int T, top_k, n_exp, dim, I, tiles_dim;
+};
+
+size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k);
+// Points h, yk, gsh, count into `work` (moe_grouped_work_bytes of a.T, a.dim,
+// a.I, a.top_k, 256-byte aligned) and sets tiles_dim.  The counters need no
+// clearing: the gate/up launch zeroes them.
+void moe_grouped_bind(MoeGroupedArgs& a, void* work);
+bool moe_grouped_supported(int dim, int I, int T, int top_k);
+// Two launches: gate/up + SwiGLU, then down + combine (gate and up of one
+// kind, down of another; the shared expert's kinds equal the routed ones).
+hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
+
 // Router: logits[t] = router_w[n_exp][dim] . x[t] (f32), stable softmax,
 // greedy top-k (strict >, lowest index wins ties), renormalised weights
 // (llm_moe.adb:136-197).  Writes top_idx/top_w [T][top_k].

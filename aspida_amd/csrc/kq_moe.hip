@@ -195,72 +195,106 @@ hipError_t launch_moe_experts(const MoeWeights& w, int T, int top_k, const float
 }
 
 // ---- router -------------------------------------------------------------------
-
-// logits[t][e] = sum_d W[e][d] x[t][d]; one wave per (t, e).
-__global__ __launch_bounds__(256) void route_logits(const float* __restrict__ W, int n_exp, int dim, int T,
-                                                    const float* __restrict__ x, float* __restrict__ logits) {
-  const int lane = threadIdx.x & 63;
-  const int job = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (job >= n_exp * T) return;
-  const int t = job / n_exp, e = job % n_exp;
-  const float4* w4 = (const float4*)(W + (size_t)e * dim);
-  const float4* x4 = (const float4*)(x + (size_t)t * dim);
-  float a = 0.f;
-  for (int i = lane; i < dim / 4; i += 64) {
-    const float4 p = w4[i], q = x4[i];
-    a = __builtin_fmaf(p.x, q.x, a);
-    a = __builtin_fmaf(p.y, q.y, a);
-    a = __builtin_fmaf(p.z, q.z, a);
-    a = __builtin_fmaf(p.w, q.w, a);
-  }
-  a = wave_sum(a);
-  if (lane == 0) logits[job] = a;
-}
-
-// Softmax + greedy top-k + renormalisation for one token per wave
-// (llm_moe.adb:153-197).  The exp-sum and the renormalising sum run
-// sequentially in ascending order, as on the CPU, so equal probabilities are
-// created exactly where the CPU creates them; the arg-max takes the lowest
-// index among equal values.
+//
+// One workgroup (4 waves) per token: logits[t][e] = W[e] . x[t] (wave w takes
+// experts w, w + 4, ...; each a coalesced dot over dim), stable softmax,
+// greedy top-k and renormalisation (llm_moe.adb:136-197).  The exp-sum and
+// the renormalising sum run sequentially in ascending order, as on the CPU,
+// so equal probabilities arise exactly where the CPU's do; the arg-max takes
+// the lowest index among equal values.
 constexpr int ROUTE_MAX_EXP = 1024;
-__global__ __launch_bounds__(64) void route_topk(const float* __restrict__ logits, int n_exp, int top_k,
-                                                 int* __restrict__ top_idx, float* __restrict__ top_w) {
+constexpr int ROUTE_MAX_DIM4 = 64 * 16;  // dim / 4 cached in registers: dim <= 4096
+
+// CACHE_X: dim <= 4096, x held in registers for all experts; otherwise x is
+// re-read (from cache) per expert.  Both add in the same order.
+template <bool CACHE_X>
+__global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, int n_exp, int dim,
+                                                 const float* __restrict__ x, int top_k,
+                                                 float* __restrict__ logits, int* __restrict__ top_idx,
+                                                 float* __restrict__ top_w) {
   __shared__ float p[ROUTE_MAX_EXP];
   __shared__ float bestv[MOE_MAX_TOPK];
-  const int t = blockIdx.x, lane = threadIdx.x;
-  const float* l = logits + (size_t)t * n_exp;
-  float m = -INFINITY;
-  for (int e = lane; e < n_exp; e += 64) m = fmaxf(m, l[e]);
+  __shared__ float sum_s;
+  const int t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n4 = dim / 4;
+  const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)t * dim);
+  float4 xv[CACHE_X ? 16 : 1];
+  if (CACHE_X) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  for (int e = lane; e < n_exp; e += 64) p[e] = expf(l[e] - m);
+    for (int i = 0; i < 16; ++i) xv[i] = lane + 64 * i < n4 ? x4[lane + 64 * i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int e = w; e < n_exp; e += 4) {
+    const float4* w4 = reinterpret_cast<const float4*>(W + (size_t)e * dim);
+    float a = 0.f;
+    if (CACHE_X) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (lane + 64 * i < n4) {
+          const float4 q = w4[lane + 64 * i];
+          a = __builtin_fmaf(q.x, xv[i].x, a);
+          a = __builtin_fmaf(q.y, xv[i].y, a);
+          a = __builtin_fmaf(q.z, xv[i].z, a);
+          a = __builtin_fmaf(q.w, xv[i].w, a);
+        }
+    } else {
+      for (int i = lane; i < n4; i += 64) {
+        const float4 q = w4[i], v = x4[i];
+        a = __builtin_fmaf(q.x, v.x, a);
+        a = __builtin_fmaf(q.y, v.y, a);
+        a = __builtin_fmaf(q.z, v.z, a);
+        a = __builtin_fmaf(q.w, v.w, a);
+      }
+    }
+    a = wave_sum(a);
+    if (lane == 0) {
+      p[e] = a;
+      if (logits) logits[(size_t)t * n_exp + e] = a;
+    }
+  }
   __syncthreads();
-  if (lane == 0) {
+  // Softmax and top-k on wave 0 (lanes hold e = lane + 64 i); every wave
+  // passes every barrier.
+  if (w == 0) {
+    float m = -INFINITY;
+    for (int e = lane; e < n_exp; e += 64) m = fmaxf(m, p[e]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    for (int e = lane; e < n_exp; e += 64) p[e] = expf(p[e] - m);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
     float sum = 0.f;
     for (int e = 0; e < n_exp; ++e) sum = sum + p[e];
-    for (int e = 0; e < n_exp; ++e) p[e] = p[e] / sum;
+    sum_s = sum;
+  }
+  __syncthreads();
+  if (w == 0) {
+    const float sum = sum_s;
+    for (int e = lane; e < n_exp; e += 64) p[e] = p[e] / sum;
   }
   __syncthreads();
   for (int k = 0; k < top_k; ++k) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int e = lane; e < n_exp; e += 64)
-      if (p[e] > bv) { bv = p[e]; bi = e; }
+    if (w == 0) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int e = lane; e < n_exp; e += 64)
+        if (p[e] > bv) { bv = p[e]; bi = e; }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oi = __shfl_xor(bi, o, 64);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if (bi >= n_exp) bi = 0;   // only when every remaining value is NaN
-    if (lane == 0) {
-      top_idx[t * top_k + k] = bi;
-      bestv[k] = bv;
-      p[bi] = -INFINITY;
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (bi >= n_exp) bi = 0;   // only when every remaining value is NaN
+      if (lane == 0) {
+        top_idx[t * top_k + k] = bi;
+        bestv[k] = bv;
+        p[bi] = -INFINITY;
+      }
     }
     __syncthreads();
   }
-  if (lane == 0) {
+  if (threadIdx.x == 0) {
     float sw = 0.f;
     for (int k = 0; k < top_k; ++k) sw = sw + bestv[k];
     for (int k = 0; k < top_k; ++k) top_w[t * top_k + k] = bestv[k] / sw;
@@ -270,9 +304,12 @@ __global__ __launch_bounds__(64) void route_topk(const float* __restrict__ logit
 hipError_t launch_moe_route(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
                             float* logits, int* top_idx, float* top_w, hipStream_t s) {
   if (n_exp > ROUTE_MAX_EXP || top_k > MOE_MAX_TOPK || top_k > n_exp || dim % 4) return hipErrorInvalidValue;
-  const int jobs = n_exp * T;
-  hipLaunchKernelGGL(route_logits, dim3((jobs + 3) / 4), dim3(256), 0, s, router_w, n_exp, dim, T, x, logits);
-  hipLaunchKernelGGL(route_topk, dim3(T), dim3(64), 0, s, logits, n_exp, top_k, top_idx, top_w);
+  if (dim / 4 <= ROUTE_MAX_DIM4)
+    hipLaunchKernelGGL(moe_route<true>, dim3(T), dim3(256), 0, s, router_w, n_exp, dim, x, top_k, logits, top_idx,
+                       top_w);
+  else
+    hipLaunchKernelGGL(moe_route<false>, dim3(T), dim3(256), 0, s, router_w, n_exp, dim, x, top_k, logits, top_idx,
+                       top_w);
   return hipGetLastError();
 }
 

@@ -60,6 +60,20 @@ __device__ __forceinline__ void load_chunks(const uint8_t* g, int lane, uint4 (&
   for (int k = 0; k < C; ++k) ch[k] = ld16(p + k * 1024);
 }
 
+// Make the compiler treat a register image as changed (it is not): a loop
+// that multiplies one super-block by several activation vectors then decodes
+// it per use instead of hoisting the whole decoded block (256 floats per
+// lane) out of the loop.
+template <class R>
+__device__ __forceinline__ void opaque_regs(R& r) {
+  static_assert(sizeof(R) % 4 == 0, "register image of whole dwords");
+  uint32_t w[sizeof(R) / 4];
+  __builtin_memcpy(w, &r, sizeof(R));
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(R) / 4); ++i) asm volatile("" : "+v"(w[i]));
+  __builtin_memcpy(&r, w, sizeof(R));
+}
+
 template <> struct Packed<Q4_K> {
   struct R { uint4 ch[9]; };
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {

@@ -277,6 +277,86 @@ def small_batch_table(torch, aa, synth, seed, stream):
     return table
 
 
+def moe_table(torch, aa, synth, seed, stream):
+    """Qwen3-MoE-style expert FFN: router f32 [128][2048],
+    128 experts of gate/up Q4_K [768][2048] and down Q6_K [2048][768] plus one
+    shared expert with a sigmoid gate, top-8, for T = 1, 8 and 32 tokens; the
+    device path (router + grouped experts over packed expert tensors),
+    rotating over three layers' weights (1.2 GB) so each layer reads cold HBM.
+    GB/s counts the weights of the E_T distinct routed experts the router
+    picked, the shared expert, the router and the activations."""
+    dev = aa.DeviceOps()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 3)
+    dim, inter, n_exp, top_k, nlayers = 2048, 768, 128, 8, 3
+    f = dict(device="cuda", dtype=torch.float32)
+    sp0 = stream.cuda_stream
+
+    def packed(kind, n, in_dim, out_dim):
+        src = synth.blocks_torch(kind, n * out_dim * in_dim // 256, generator=g)
+        dst = torch.empty(n * dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+        dev.pack_experts(kind, src.data_ptr(), src.numel() // n, in_dim, out_dim, n, dst.data_ptr(), sp0)
+        stream.synchronize()
+        del src
+        return dst
+
+    layers = []
+    for _ in range(nlayers):
+        layers.append({"router": torch.randn(n_exp, dim, generator=g, **f) * 0.02,
+                       "sgi": torch.randn(dim, generator=g, **f) * 0.02,
+                       "gate": packed(aa.Q4_K, n_exp, dim, inter), "up": packed(aa.Q4_K, n_exp, dim, inter),
+                       "down": packed(aa.Q6_K, n_exp, inter, dim), "shg": packed(aa.Q4_K, 1, dim, inter),
+                       "shu": packed(aa.Q4_K, 1, dim, inter), "shd": packed(aa.Q6_K, 1, inter, dim)})
+    gs = aa.weight_bytes(aa.Q4_K, dim, inter)
+    ds = aa.weight_bytes(aa.Q6_K, inter, dim)
+    per_expert = 2 * gs + ds
+    table = {}
+    for T in (1, 8, 32):
+        X = torch.randn(T, dim, generator=g, **f)
+        bufs = [{"logits": torch.empty(T, n_exp, **f), "idx": torch.empty(T, top_k, device="cuda", dtype=torch.int32),
+                 "tw": torch.empty(T, top_k, **f),
+                 "work": torch.empty(dev.moe_packed_work_bytes(T, dim, inter, top_k), dtype=torch.uint8,
+                                     device="cuda"),
+                 "y": torch.empty(T, dim, **f)} for _ in range(nlayers)]
+
+        def run(sp):
+            for L, B in zip(layers, bufs):
+                dev.route(L["router"].data_ptr(), n_exp, dim, T, top_k, X.data_ptr(), B["logits"].data_ptr(),
+                          B["idx"].data_ptr(), B["tw"].data_ptr(), sp)
+                dev.moe_experts_packed(X.data_ptr(), T, dim, top_k, inter, n_exp, B["idx"].data_ptr(),
+                                       B["tw"].data_ptr(), L["gate"].data_ptr(), L["up"].data_ptr(), aa.Q4_K,
+                                       L["down"].data_ptr(), aa.Q6_K, L["shg"].data_ptr(), L["shu"].data_ptr(),
+                                       L["shd"].data_ptr(), L["sgi"].data_ptr(), B["work"].data_ptr(),
+                                       B["y"].data_ptr(), sp)
+
+        with torch.cuda.stream(stream):
+            run(stream.cuda_stream)
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                run(stream.cuda_stream)
+            graph.replay()
+            stream.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            stream.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / (reps * nlayers)
+        distinct = sum(len(set(B["idx"].cpu().numpy().ravel().tolist())) for B in bufs) / nlayers
+        nbytes = (distinct + 1) * per_expert + n_exp * dim * 4 + 4 * T * (2 * dim)
+        table[f"T={T}"] = {"us": round(t * 1e6, 2), "distinct_experts": round(distinct, 1),
+                           "GBps": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3)}
+        print(f"# MoE T={T}: {t * 1e6:.2f} us, E_T={distinct:.1f}, {nbytes / t / 1e9:.0f} GB/s",
+              file=sys.stderr, flush=True)
+        del graph, bufs
+    del layers
+    torch.cuda.empty_cache()
+    return table
+
+
 def cpu_baseline(seed, threads):
     """Aspida's CPU QMatVec (restated in C, pooled rows as LLM_Pool does) on the
     same decode stream, timed on a bounded sample: one layer's seven matvecs
@@ -392,6 +472,7 @@ def main():
         del a, b
     table = None if args.no_table else kquant_table(torch, aa, synth, args.seed, stream)
     small = None if args.no_table else small_batch_table(torch, aa, synth, args.seed, stream)
+    moe = None if args.no_table else moe_table(torch, aa, synth, args.seed, stream)
     del dec
     torch.cuda.empty_cache()
 
@@ -416,6 +497,7 @@ def main():
         "kernels": groups,
         "kquant_matvec": table,
         "small_batch_mfma": small,
+        "moe_layer": moe,
     }
     assert dec_bytes_ok(stream_bytes), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"
     print(json.dumps(line), flush=True)

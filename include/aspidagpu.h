@@ -57,7 +57,10 @@ void aspida_gpu_free_weight(const void *w);
  * shared_gate_inp is non-null, else 1.  Routed expert tensors are
  * [n_exp][rows][cols] with bytes / n_exp per expert.  Replaces
  * gpu/gpu_matvec.cu:1673-1758; top_k may be up to 32 (the reference silently
- * truncated it to 8); dim and intermed must be multiples of 256. */
+ * truncated it to 8); dim and intermed must be multiples of 256.  When gate,
+ * up, shared gate and shared up share one kind and down and shared down
+ * another, the experts are mirrored in the packed layout and run by the
+ * grouped kernels of aspida_moe_experts_packed_dev. */
 void aspida_gpu_moe_experts(const float *x, int dim, int top_k, int intermed, int n_exp,
                             const int *top_idx, const float *top_w,
                             const void *gate_w, long gate_bytes, int gate_kind,
@@ -171,6 +174,26 @@ int aspida_moe_experts_dev(const float *x, int T, int dim, int top_k, int interm
                            const void *shg_w, int shg_kind, const void *shu_w, int shu_kind,
                            const void *shd_w, int shd_kind, const float *shared_gate_inp,
                            float *work, float *y, void *stream);
+
+/* Grouped MoE over packed experts.  Same arithmetic contract as
+ * aspida_moe_experts_dev (LLM_MoE.Forward steps 4-5,
+ * src/llm/llm_moe.adb:249-299; the reference shim's moe_experts,
+ * gpu/gpu_matvec.cu:1673-1760), but the expert matrices are in the packed
+ * layout (aspida_moe_pack_experts_dev) and each expert's weights are read once
+ * per launch however many of the T tokens chose it.  Gate, up, shared gate
+ * and shared up are of kind gu_kind, down and shared down of down_kind.
+ * dim and intermed multiples of 256, top_k <= 32.  x 16-byte aligned, work
+ * 256-byte aligned with aspida_moe_packed_work_bytes bytes.  Deterministic:
+ * each y[t] sums its slots in ascending k, shared expert last.  top_idx
+ * entries outside [0, n_exp) leave that token's y unwritten. */
+long aspida_moe_packed_work_bytes(int T, int dim, int intermed, int top_k);
+int aspida_moe_pack_experts_dev(int kind, const void *src, long src_stride, int in_dim, int out_dim, int n,
+                                void *dst, void *stream);
+int aspida_moe_experts_packed_dev(const float *x, int T, int dim, int top_k, int intermed, int n_exp,
+                                  const int *top_idx, const float *top_w, const void *gate_p,
+                                  const void *up_p, int gu_kind, const void *down_p, int down_kind,
+                                  const void *shg_p, const void *shu_p, const void *shd_p,
+                                  const float *shared_gate_inp, void *work, float *y, void *stream);
 
 /* Launch-shape override for batch-1 matvecs: rows per lane group per step
  * (1, 2 or 4) and resident waves launched per CU (1..64); rows_per_wave <= 0

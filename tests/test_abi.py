@@ -99,3 +99,35 @@ def test_device_entry_points_reject_bad_arguments(lib):
     assert lib.aspida_kq_set_mv_config(2, 0) < 0
     assert lib.aspida_kq_set_mv_config(0, 16) == 0
     assert lib.aspida_moe_work_floats(1, 2048, 8, 768) > 9 * 768 * 3
+
+
+def test_grouped_moe_rejects_bad_arguments(lib):
+    """aspida_moe_experts_packed_dev validates before any launch (the fake
+    pointers are never dereferenced)."""
+    assert lib.aspida_moe_packed_work_bytes(0, 2048, 768, 8) < 0
+    assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 33) < 0
+    # one token: h 9 x 768, yk 9 x 2048 floats, gsh, 32 tile counters of 256 B
+    assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 8) == 4 * 9 * (768 + 2048) + 256 + 32 * 256
+    # T * top_k above the per-launch job bound: sized for one chunk of 128 tokens
+    assert lib.aspida_moe_packed_work_bytes(1000, 2048, 768, 8) == lib.aspida_moe_packed_work_bytes(128, 2048, 768, 8)
+    one = 256
+    args = dict(x=one, T=1, dim=2048, top_k=8, intermed=768, n_exp=128, idx=one, tw=one, g=one, u=one, gk=0, d=one,
+                dk=1, sg=one, su=one, sd=one, sgi=None, work=one, y=one)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.aspida_moe_experts_packed_dev(a["x"], a["T"], a["dim"], a["top_k"], a["intermed"], a["n_exp"],
+                                                 a["idx"], a["tw"], a["g"], a["u"], a["gk"], a["d"], a["dk"],
+                                                 a["sg"], a["su"], a["sd"], a["sgi"], a["work"], a["y"], None)
+    assert call(dim=2000) < 0
+    assert call(intermed=700) < 0
+    assert call(top_k=129) < 0
+    assert call(top_k=0) < 0
+    assert call(T=0) < 0
+    assert call(x=None) < 0
+    assert call(gk=9) < 0
+    assert call(dk=-1) < 0
+    assert call(x=one + 4) < 0          # x must be 16-byte aligned
+    assert call(work=one + 16) < 0      # work must be 256-byte aligned
+    assert lib.aspida_moe_pack_experts_dev(0, one, 10, 256, 64, 2, one, None) < 0   # stride below one matrix
+    assert lib.aspida_moe_pack_experts_dev(0, one, 64 * 144, 300, 64, 2, one, None) < 0

@@ -151,3 +151,95 @@ def test_moe_layer_device_path(T):
         want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, gi[t], gw[t], L["gate"], L["up"], L["down"],
                                   L["shg"], L["shu"], L["shd"], shared_gate_inp=L["sgi"], nthreads=ncpu())
         _assert_moe(gy[t], want, f"T={T} token {t}")
+
+
+# ---- grouped experts over packed expert tensors -------------------------------
+
+PACKED_CASES = [
+    # dim, inter, n_exp, top_k, gate/up kind, down kind, gated, T
+    (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 1),     # the benchmark layer
+    (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 8),
+    (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, False, 32),
+    (1536, 512, 4, 3, aa.Q5_K, aa.Q3_K, True, 40),      # 6 columns: 3 waves x 2; ~30 jobs per expert
+    (1792, 1792, 5, 2, aa.Q2_K, aa.Q8_0, False, 9),     # 7 columns: 1 wave x 7
+    (256, 256, 3, 2, aa.Q6_K, aa.Q4_K, True, 130),      # one column; 87 jobs per expert
+    (512, 768, 8, 4, aa.Q8_0, aa.Q5_K, True, 300),      # T * top_k > 1024: two launches
+]
+
+
+def _packed_experts(dev, kind, host, in_dim, out_dim, n):
+    """Upload n ggml matrices (host array of n * rows) and pack them."""
+    torch = torch_cuda()
+    src = to_dev(host)
+    pb = dev.packed_bytes(kind, in_dim, out_dim)
+    dst = torch.empty(n * pb, dtype=torch.uint8, device="cuda")
+    dev.pack_experts(kind, src.data_ptr(), host.size // n, in_dim, out_dim, n, dst.data_ptr(), stream())
+    return dst, src
+
+
+def _run_packed(dev, L, dim, inter, n_exp, top_k, gk, dk, gated, X, idx, tw):
+    torch = torch_cuda()
+    T = X.shape[0]
+    keep = []
+    P = {}
+    for name, in_dim, out_dim, n in (("gate", dim, inter, n_exp), ("up", dim, inter, n_exp),
+                                     ("down", inter, dim, n_exp), ("shg", dim, inter, 1),
+                                     ("shu", dim, inter, 1), ("shd", inter, dim, 1)):
+        arr, kind = L[name]
+        p, s = _packed_experts(dev, kind, arr, in_dim, out_dim, n)
+        P[name] = p.data_ptr()
+        keep += [p, s]
+    dX, dI, dW = to_dev(X), to_dev(idx.astype(np.int32)), to_dev(tw.astype(np.float32))
+    dS = to_dev(L["sgi"]) if gated else None
+    work = torch.empty(dev.moe_packed_work_bytes(T, dim, inter, top_k), dtype=torch.uint8, device="cuda")
+    outs = []
+    for _ in range(2):
+        y = torch.full((T, dim), float("nan"), dtype=torch.float32, device="cuda")
+        dev.moe_experts_packed(dX.data_ptr(), T, dim, top_k, inter, n_exp, dI.data_ptr(), dW.data_ptr(),
+                               P["gate"], P["up"], gk, P["down"], dk, P["shg"], P["shu"], P["shd"],
+                               dS.data_ptr() if gated else None, work.data_ptr(), y.data_ptr(), stream())
+        sync()
+        outs.append(y.cpu().numpy())
+    return outs
+
+
+@pytest.mark.parametrize("case", PACKED_CASES,
+                         ids=lambda c: f"d{c[0]}i{c[1]}e{c[2]}k{c[3]}g{c[4]}d{c[5]}s{int(c[6])}T{c[7]}")
+def test_moe_experts_packed(case):
+    """Every token of the grouped launch against the oracle's Forward, and two
+    launches bit-identical (the combine sums in ascending k whatever the
+    arrival order)."""
+    dim, inter, n_exp, top_k, gk, dk, gated, T = case
+    dev = aa.DeviceOps()
+    gen = synth.rng(1500 + dim + inter + T)
+    L = _layer(gen, dim, inter, n_exp, gk, gk, dk)
+    X = synth.activations_np(T * dim, gen).reshape(T, dim)
+    idx = np.zeros((T, top_k), np.int32)
+    tw = np.zeros((T, top_k), np.float32)
+    for t in range(T):
+        logits = gen.standard_normal(n_exp).astype(np.float32)
+        idx[t], tw[t] = oracle.route(logits, top_k)
+    y1, y2 = _run_packed(dev, L, dim, inter, n_exp, top_k, gk, dk, gated, X, idx, tw)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), "grouped MoE not deterministic"
+    sgi = L["sgi"] if gated else None
+    for t in range(T):
+        want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, idx[t], tw[t], L["gate"], L["up"], L["down"],
+                                  L["shg"], L["shu"], L["shd"], shared_gate_inp=sgi, nthreads=ncpu())
+        _assert_moe(y1[t], want, f"T={T} token {t}")
+
+
+def test_moe_experts_packed_repeated_expert():
+    """A token that lists one expert in two slots gets both contributions."""
+    dim, inter, n_exp, top_k = 512, 256, 4, 3
+    dev = aa.DeviceOps()
+    gen = synth.rng(1777)
+    L = _layer(gen, dim, inter, n_exp)
+    X = synth.activations_np(2 * dim, gen).reshape(2, dim)
+    idx = np.array([[2, 2, 0], [1, 3, 1]], np.int32)
+    tw = np.array([[0.5, 0.3, 0.2], [0.6, 0.1, 0.3]], np.float32)
+    y, _ = _run_packed(dev, L, dim, inter, n_exp, top_k, aa.Q4_K, aa.Q6_K, True, X, idx, tw)
+    for t in range(2):
+        want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, idx[t], tw[t], L["gate"], L["up"], L["down"],
+                                  L["shg"], L["shu"], L["shd"], shared_gate_inp=L["sgi"], nthreads=ncpu())
+        _assert_moe(y[t], want, f"token {t}")
+
