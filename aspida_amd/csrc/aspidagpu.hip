@@ -406,7 +406,7 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
   // Grouped path over packed experts when gate, up and the shared gate/up
   // share one kind and both downs another (the Q4_K_M layouts do).
   if (gate_kind == up_kind && shg_kind == gate_kind && shu_kind == gate_kind && shd_kind == down_kind &&
-      kq::moe_grouped_supported(dim, intermed, 1, top_k)) {
+      kq::moe_grouped_supported(dim, intermed, 1, top_k) && kq::moe_grouped_experts_ok(n_exp)) {
     kq::MoeGroupedArgs a{};
     // The per-expert stride of the host tensors is bytes / n_exp (gpu_matvec.cu:1702-1703).
     a.gate = (const uint8_t*)packed_weight(gate_w, gate_kind, dim, intermed, n_exp, (size_t)(gate_bytes / n_exp));
@@ -633,9 +633,14 @@ extern "C" int aspida_dense_matvec_dev(const float* w, int in_dim, int out_dim, 
 
 extern "C" int aspida_moe_route_dev(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
                                     float* logits, int* top_idx, float* top_w, void* stream) {
-  if (!router_w || !x || !logits || !top_idx || !top_w || n_exp <= 0 || dim <= 0 || T <= 0 || top_k <= 0)
+  if (!router_w || !x || !logits || !top_idx || !top_w || n_exp <= 0 || dim <= 0 || dim % 4 || T <= 0 ||
+      top_k <= 0 || ((uintptr_t)router_w & 15) || ((uintptr_t)x & 15))
     return -EINVAL;
-  return check(kq::launch_moe_route(router_w, n_exp, dim, T, top_k, x, logits, top_idx, top_w,
+  // Arrival counters from the stream's matvec workspace (one per 64 "rows",
+  // kept zero between launches).
+  MvWorkspace* ws = stream_workspace(stream, 256, kq::moe_route_groups(T) * 64, 1);
+  if (!ws) return t_last_error ? t_last_error : -1;
+  return check(kq::launch_moe_route(router_w, n_exp, dim, T, top_k, x, logits, top_idx, top_w, ws->count.p,
                                     (hipStream_t)stream),
                "aspida_moe_route_dev");
 }
@@ -705,6 +710,7 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
   const bool ok = x && top_idx && top_w && gate_p && up_p && down_p && shg_p && shu_p && shd_p && work && y &&
                   valid_kind(gu_kind) && valid_kind(down_kind) && T > 0 && n_exp > 0 && top_k > 0 &&
                   top_k <= n_exp && kq::moe_grouped_supported(dim, intermed, 1, top_k) &&
+                  kq::moe_grouped_experts_ok(n_exp) &&
                   ((uintptr_t)x & 15) == 0 && ((uintptr_t)work & 255) == 0;
   if (!ok) return -EINVAL;
   kq::MoeGroupedArgs a{};

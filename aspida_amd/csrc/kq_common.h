@@ -70,6 +70,70 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+
+// DPP lane moves within a wave (no LDS round trip).  dpp_from(v, ctrl, old):
+// the value of the source lane that ctrl names, or `old` where there is none.
+// Controls: row_shr:n = 0x110 + n (from lane - n within a row of 16),
+// row_bcast:15 = 0x142 (lane 15 of the previous row, rows 1 and 3),
+// row_bcast:31 = 0x143 (lane 31, rows 2 and 3).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_from(int v, int old) {
+  return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_from(float v, float old) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xF, false));
+}
+
+// Inclusive scan over the 64 lanes (lane l gets v_0 + ... + v_l, added in a
+// fixed order); lane 63 holds the total.
+template <class T>
+__device__ __forceinline__ T wave_scan_add(T v) {
+  v += dpp_from<0x111>(v, T(0));
+  v += dpp_from<0x112>(v, T(0));
+  v += dpp_from<0x114>(v, T(0));
+  v += dpp_from<0x118>(v, T(0));
+  v += dpp_from<0x142, 0xA>(v, T(0));
+  v += dpp_from<0x143, 0xC>(v, T(0));
+  return v;
+}
+
+// The wave total, in every lane.
+__device__ __forceinline__ float wave_total(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_scan_add(v)), 63));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_from<0x111>(v, v));
+  v = fmaxf(v, dpp_from<0x112>(v, v));
+  v = fmaxf(v, dpp_from<0x114>(v, v));
+  v = fmaxf(v, dpp_from<0x118>(v, v));
+  v = fmaxf(v, dpp_from<0x142, 0xA>(v, v));
+  v = fmaxf(v, dpp_from<0x143, 0xC>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Arg-max over the wave: the largest v, the lowest index among equals
+// (NaN never wins; with only NaN left the index stays 0x7fffffff).  Result in
+// every lane.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#define KQ_ARGMAX_STEP(CTRL, RM)                                   \
+  {                                                                \
+    const float ov = dpp_from<CTRL, RM>(v, v);                     \
+    const int oi = dpp_from<CTRL, RM>(i, i);                       \
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }         \
+  }
+  KQ_ARGMAX_STEP(0x111, 0xF)
+  KQ_ARGMAX_STEP(0x112, 0xF)
+  KQ_ARGMAX_STEP(0x114, 0xF)
+  KQ_ARGMAX_STEP(0x118, 0xF)
+  KQ_ARGMAX_STEP(0x142, 0xA)
+  KQ_ARGMAX_STEP(0x143, 0xC)
+#undef KQ_ARGMAX_STEP
+  v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  i = __builtin_amdgcn_readlane(i, 63);
+}
 #endif
 
 }  // namespace kq

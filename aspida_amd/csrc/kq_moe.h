@@ -39,8 +39,10 @@ hipError_t launch_moe_experts(const MoeWeights& w, int T, int top_k, const float
 
 // ---- grouped path over packed expert weights (kq_moe_grouped.hip) ----
 
-// Jobs (token, slot) one expert can serve per launch (T * top_k bound).
+// Routed jobs (token, slot) per launch (T * top_k bound; also T <= it).
 constexpr int MOE_MAX_JOBS = 1024;
+// Routed experts the grouped path schedules (LDS tables per workgroup).
+constexpr int MOE_MAX_EXP = 1024;
 
 // Packed expert tensors: expert e's matrix at base + e * stride (stride =
 // packed bytes of one [rows][cols] matrix); the shared expert's matrices
@@ -64,6 +66,7 @@ size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k);
 // clearing: the gate/up launch zeroes them.
 void moe_grouped_bind(MoeGroupedArgs& a, void* work);
 bool moe_grouped_supported(int dim, int I, int T, int top_k);
+bool moe_grouped_experts_ok(int n_exp);
 // Two launches: gate/up + SwiGLU, then down + combine (gate and up of one
 // kind, down of another; the shared expert's kinds equal the routed ones).
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
@@ -71,7 +74,11 @@ hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kin
 // Router: logits[t] = router_w[n_exp][dim] . x[t] (f32), stable softmax,
 // greedy top-k (strict >, lowest index wins ties), renormalised weights
 // (llm_moe.adb:136-197).  Writes top_idx/top_w [T][top_k].
+// count: moe_route_groups(T) zeroed counters, 64 unsigned (256 bytes) apart;
+// every launch leaves them zero again.  Launches sharing counters must be
+// ordered (one stream).  logits is required (the selection reads it back).
 hipError_t launch_moe_route(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
-                            float* logits, int* top_idx, float* top_w, hipStream_t s);
+                            float* logits, int* top_idx, float* top_w, unsigned* count, hipStream_t s);
+int moe_route_groups(int T);
 
 }  // namespace kq

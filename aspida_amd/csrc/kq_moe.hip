@@ -15,6 +15,7 @@
 #include "kq_blocks.h"
 #include "kq_kernels.h"
 #include "kq_moe.h"
+#include "kq_packed.h"
 
 namespace kq {
 
@@ -196,120 +197,152 @@ hipError_t launch_moe_experts(const MoeWeights& w, int T, int top_k, const float
 
 // ---- router -------------------------------------------------------------------
 //
-// One workgroup (4 waves) per token: logits[t][e] = W[e] . x[t] (wave w takes
-// experts w, w + 4, ...; each a coalesced dot over dim), stable softmax,
-// greedy top-k and renormalisation (llm_moe.adb:136-197).  The exp-sum and
-// the renormalising sum run sequentially in ascending order, as on the CPU,
-// so equal probabilities arise exactly where the CPU's do; the arg-max takes
-// the lowest index among equal values.
+// logits[t][e] = W[e] . x[t], stable softmax, greedy top-k and
+// renormalisation (llm_moe.adb:136-197).  Workgroup (i, j) of 4 waves takes
+// experts 4i..4i+3 (one per wave) for tokens ROUTE_TT j .. ROUTE_TT j + 3, so
+// the router matrix is spread over many CUs and each row is read once per
+// token group.  The logits are published with device-scope stores; the last
+// workgroup of a token group to arrive (a per-group counter, reset by that
+// workgroup) runs the selection, one wave per token.  The selection follows
+// the CPU's rule exactly -- strict >, so the lowest index wins among equal
+// probabilities -- on probabilities that may differ from the CPU's in the last
+// bits (the exponential and the order of the exp-sum differ), as any GPU
+// softmax does.
 constexpr int ROUTE_MAX_EXP = 1024;
-constexpr int ROUTE_MAX_DIM4 = 64 * 16;  // dim / 4 cached in registers: dim <= 4096
+constexpr int ROUTE_TT = 4;
 
-// CACHE_X: dim <= 4096, x held in registers for all experts; otherwise x is
-// re-read (from cache) per expert.  Both add in the same order.
-template <bool CACHE_X>
-__global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, int n_exp, int dim,
-                                                 const float* __restrict__ x, int top_k,
-                                                 float* __restrict__ logits, int* __restrict__ top_idx,
-                                                 float* __restrict__ top_w) {
-  __shared__ float p[ROUTE_MAX_EXP];
-  __shared__ float bestv[MOE_MAX_TOPK];
-  __shared__ float sum_s;
-  const int t = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n4 = dim / 4;
-  const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)t * dim);
-  float4 xv[CACHE_X ? 16 : 1];
-  if (CACHE_X) {
+// Softmax + top-k of one token's logits lg[0..n_exp) by one wave; lane l holds
+// experts l, l + 64, ..., PER of them (n_exp <= 64 PER).  Lane k < top_k
+// writes slot k.
+template <int PER>
+__device__ __forceinline__ void route_select(const float* lg, int n_exp, int top_k, int lane, int* __restrict__ idx,
+                                             float* __restrict__ tw) {
+  float p[PER];
+  float m = -INFINITY;
+  // All loads issued before any use: indices clamped instead of branched on.
 #pragma unroll
-    for (int i = 0; i < 16; ++i) xv[i] = lane + 64 * i < n4 ? x4[lane + 64 * i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = __hip_atomic_load(lg + (e < n_exp ? e : n_exp - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  for (int e = w; e < n_exp; e += 4) {
-    const float4* w4 = reinterpret_cast<const float4*>(W + (size_t)e * dim);
-    float a = 0.f;
-    if (CACHE_X) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (lane + 64 * i < n4) {
-          const float4 q = w4[lane + 64 * i];
-          a = __builtin_fmaf(q.x, xv[i].x, a);
-          a = __builtin_fmaf(q.y, xv[i].y, a);
-          a = __builtin_fmaf(q.z, xv[i].z, a);
-          a = __builtin_fmaf(q.w, xv[i].w, a);
-        }
-    } else {
-      for (int i = lane; i < n4; i += 64) {
-        const float4 q = w4[i], v = x4[i];
-        a = __builtin_fmaf(q.x, v.x, a);
-        a = __builtin_fmaf(q.y, v.y, a);
-        a = __builtin_fmaf(q.z, v.z, a);
-        a = __builtin_fmaf(q.w, v.w, a);
-      }
-    }
-    a = wave_sum(a);
-    if (lane == 0) {
-      p[e] = a;
-      if (logits) logits[(size_t)t * n_exp + e] = a;
-    }
+  for (int i = 0; i < PER; ++i) {
+    if (lane + 64 * i >= n_exp) p[i] = -INFINITY;
+    m = fmaxf(m, p[i]);
   }
-  __syncthreads();
-  // Softmax and top-k on wave 0 (lanes hold e = lane + 64 i); every wave
-  // passes every barrier.
-  if (w == 0) {
-    float m = -INFINITY;
-    for (int e = lane; e < n_exp; e += 64) m = fmaxf(m, p[e]);
+  m = wave_max(m);
+  float part = 0.f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    for (int e = lane; e < n_exp; e += 64) p[e] = expf(p[e] - m);
+  for (int i = 0; i < PER; ++i) {
+    p[i] = lane + 64 * i < n_exp ? expf(p[i] - m) : 0.f;
+    part += p[i];
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = 0.f;
-    for (int e = 0; e < n_exp; ++e) sum = sum + p[e];
-    sum_s = sum;
-  }
-  __syncthreads();
-  if (w == 0) {
-    const float sum = sum_s;
-    for (int e = lane; e < n_exp; e += 64) p[e] = p[e] / sum;
-  }
-  __syncthreads();
+  const float sum = wave_total(part);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) p[i] = lane + 64 * i < n_exp ? p[i] / sum : -INFINITY;
+  float mine_v = 0.f;
+  int mine_i = 0;
   for (int k = 0; k < top_k; ++k) {
-    if (w == 0) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int e = lane; e < n_exp; e += 64)
-        if (p[e] > bv) { bv = p[e]; bi = e; }
+    // This lane's best (strict >: the lowest of its experts among equals,
+    // never NaN), then the wave's.
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-      if (bi >= n_exp) bi = 0;   // only when every remaining value is NaN
-      if (lane == 0) {
-        top_idx[t * top_k + k] = bi;
-        bestv[k] = bv;
-        p[bi] = -INFINITY;
-      }
-    }
-    __syncthreads();
+    for (int i = 0; i < PER; ++i)
+      if (p[i] > bv) { bv = p[i]; bi = lane + 64 * i; }
+    wave_argmax(bv, bi);
+    if (bi >= n_exp) bi = 0;  // only when every remaining value is NaN
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (bi == lane + 64 * i) p[i] = -INFINITY;
+    if (lane == k) { mine_v = bv; mine_i = bi; }
   }
-  if (threadIdx.x == 0) {
-    float sw = 0.f;
-    for (int k = 0; k < top_k; ++k) sw = sw + bestv[k];
-    for (int k = 0; k < top_k; ++k) top_w[t * top_k + k] = bestv[k] / sw;
+  // Renormalise by the sum of the selected probabilities, in ascending k.
+  float sw = 0.f;
+  for (int k = 0; k < top_k; ++k) sw = sw + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine_v), k));
+  if (lane < top_k) {
+    idx[lane] = mine_i;
+    tw[lane] = mine_v / sw;
   }
 }
 
+__global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, int n_exp, int dim, int T,
+                                                 const float* __restrict__ x, int top_k, float* __restrict__ logits,
+                                                 int* __restrict__ top_idx, float* __restrict__ top_w,
+                                                 unsigned* __restrict__ count) {
+  __shared__ int last;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e = blockIdx.x * 4 + w;
+  const int t0 = blockIdx.y * ROUTE_TT;
+  const int nt = T - t0 < ROUTE_TT ? T - t0 : ROUTE_TT;
+  const int n4 = dim / 4;
+  if (e < n_exp) {
+    // Rows are read in blocks of RB float4 per lane, all loads of a block in
+    // flight together: indices are clamped (and the products of the padding
+    // zeroed) instead of branched on, and absent tokens re-read token t0.
+    constexpr int RB = 8;
+    const float4* w4 = reinterpret_cast<const float4*>(W + (size_t)e * dim);
+    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)t0 * dim);
+    float acc[ROUTE_TT] = {0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < n4; b += 64 * RB) {
+      float4 q[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int i = b + 64 * r + lane;
+        const float4 v = w4[i < n4 ? i : n4 - 1];
+        q[r] = i < n4 ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int tt = 0; tt < ROUTE_TT; ++tt) {
+        const float4* xt = x4 + (size_t)(tt < nt ? tt : 0) * n4;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          const int i = b + 64 * r + lane;
+          const float4 v = xt[i < n4 ? i : n4 - 1];
+          acc[tt] = __builtin_fmaf(q[r].x, v.x, acc[tt]);
+          acc[tt] = __builtin_fmaf(q[r].y, v.y, acc[tt]);
+          acc[tt] = __builtin_fmaf(q[r].z, v.z, acc[tt]);
+          acc[tt] = __builtin_fmaf(q[r].w, v.w, acc[tt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < ROUTE_TT; ++tt) {
+      const float s = wave_total(acc[tt]);
+      if (lane == 0 && tt < nt)
+        __hip_atomic_store(&logits[(size_t)(t0 + tt) * n_exp + e], s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the logits stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* c = count + (size_t)blockIdx.y * COUNTER_STRIDE;
+    const bool l = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    if (l) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next launch
+    last = l;
+  }
+  __syncthreads();
+  if (!last || w >= nt) return;
+  const int t = t0 + w;
+  const float* lg = logits + (size_t)t * n_exp;
+  int* ti = top_idx + (size_t)t * top_k;
+  float* tw = top_w + (size_t)t * top_k;
+  if (n_exp <= 64) route_select<1>(lg, n_exp, top_k, lane, ti, tw);
+  else if (n_exp <= 128) route_select<2>(lg, n_exp, top_k, lane, ti, tw);
+  else if (n_exp <= 256) route_select<4>(lg, n_exp, top_k, lane, ti, tw);
+  else route_select<ROUTE_MAX_EXP / 64>(lg, n_exp, top_k, lane, ti, tw);
+}
+
+int moe_route_groups(int T) { return (T + ROUTE_TT - 1) / ROUTE_TT; }
+
 hipError_t launch_moe_route(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
-                            float* logits, int* top_idx, float* top_w, hipStream_t s) {
-  if (n_exp > ROUTE_MAX_EXP || top_k > MOE_MAX_TOPK || top_k > n_exp || dim % 4) return hipErrorInvalidValue;
-  if (dim / 4 <= ROUTE_MAX_DIM4)
-    hipLaunchKernelGGL(moe_route<true>, dim3(T), dim3(256), 0, s, router_w, n_exp, dim, x, top_k, logits, top_idx,
-                       top_w);
-  else
-    hipLaunchKernelGGL(moe_route<false>, dim3(T), dim3(256), 0, s, router_w, n_exp, dim, x, top_k, logits, top_idx,
-                       top_w);
+                            float* logits, int* top_idx, float* top_w, unsigned* count, hipStream_t s) {
+  if (n_exp > ROUTE_MAX_EXP || top_k > MOE_MAX_TOPK || top_k > n_exp || top_k > 64 || dim % 4 || !logits || !count)
+    return hipErrorInvalidValue;
+  const dim3 grid((n_exp + 3) / 4, (T + ROUTE_TT - 1) / ROUTE_TT);
+  hipLaunchKernelGGL(moe_route, grid, dim3(256), 0, s, router_w, n_exp, dim, T, x, top_k, logits, top_idx, top_w,
+                     count);
   return hipGetLastError();
 }
 

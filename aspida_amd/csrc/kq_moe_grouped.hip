@@ -23,31 +23,39 @@
 // v_fma_mix_f32), so no xsum launch is needed.
 #include <math.h>
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+
 #include "kq_moe.h"
 #include "kq_packed.h"
 
 namespace kq {
 
-constexpr int MOE_JOBS_PER_PASS = 8;  // jobs whose partial sums share LDS at once
 
-// s16[j] = sum of xs[16j .. 16j+15] (wave-uniform); xs 16-byte aligned.
-__device__ __forceinline__ void moe_sb_sums(const float* __restrict__ xs, int lane, float (&s16)[16]) {
-  float4 v;
-  __builtin_memcpy(&v, __builtin_assume_aligned(xs + 4 * lane, 16), 16);
+// Each wave multiplies its weight column by one job's 256 activations at a
+// time.  The lane's float4 of them is loaded from HBM/L2 one job ahead,
+// written to the wave's own LDS slot and read back by every lane (broadcast),
+// so a job costs one short LDS round trip instead of a chain of dependent
+// global loads.  Within a wave, LDS operations complete in program order, so
+// the slot needs no workgroup barrier; wave_barrier keeps the compiler from
+// moving the reads above the write.
+__device__ __forceinline__ void moe_stage(float4 v, float* __restrict__ slot, int lane, float (&s16)[16]) {
+  __builtin_amdgcn_wave_barrier();
+  *reinterpret_cast<float4*>(slot + 4 * lane) = v;
   float t = (v.x + v.y) + (v.z + v.w);
   t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, false));
   t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, false));
 #pragma unroll
   for (int j = 0; j < 16; ++j)
     s16[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 4 * j));
+  __builtin_amdgcn_wave_barrier();
 }
 
 template <int KIND>
-__device__ __forceinline__ float moe_sb_dot(const typename Packed<KIND>::R& r, const float* __restrict__ xs,
-                                            int lane) {
+__device__ __forceinline__ float moe_dot(const typename Packed<KIND>::R& r, const float* __restrict__ xs,
+                                         const float (&s16)[16]) {
   using B = Block<KIND>;
-  float s16[16];
-  moe_sb_sums(xs, lane, s16);
   float acc = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -58,14 +66,11 @@ __device__ __forceinline__ float moe_sb_dot(const typename Packed<KIND>::R& r, c
   return acc;
 }
 
-// The gate and up dots of one super-block column over the same activations:
-// each quarter of x is loaded once (64 SGPRs) and feeds both matrices.
+// The gate and up dots over the same staged activations.
 template <int KIND>
-__device__ __forceinline__ float2 moe_sb_dot2(const typename Packed<KIND>::R& rg, const typename Packed<KIND>::R& ru,
-                                              const float* __restrict__ xs, int lane) {
+__device__ __forceinline__ float2 moe_dot2(const typename Packed<KIND>::R& rg, const typename Packed<KIND>::R& ru,
+                                           const float* __restrict__ xs, const float (&s16)[16]) {
   using B = Block<KIND>;
-  float s16[16];
-  moe_sb_sums(xs, lane, s16);
   float g = 0.f, u = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -73,108 +78,189 @@ __device__ __forceinline__ float2 moe_sb_dot2(const typename Packed<KIND>::R& rg
     B::load_x(xs, s16, q, X);
     g += B::dot(Packed<KIND>::quarter(rg, q), q, X);
     u += B::dot(Packed<KIND>::quarter(ru, q), q, X);
-    // Keep the next quarter's scalar loads below this one's arithmetic:
-    // hoisted, the four quarters (256 SGPRs) spill into vector lanes.
-    asm volatile("" ::: "memory");
   }
   return make_float2(g, u);
 }
 
-// Jobs (t * slots + k) of expert e, in ascending job order: routed slots with
-// top_idx[t][k] == e, or every token's shared slot for e == n_exp.  Wave 0
-// compacts 64 routing entries per step with a ballot.
-__device__ __forceinline__ int moe_jobs(const int* __restrict__ idx, int T, int top_k, int n_exp, int e,
-                                        int* __restrict__ jobs) {
-  __shared__ int nj;
-  const int slots = top_k + 1;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    if (e == n_exp) {
-      for (int t = lane; t < T; t += 64) jobs[t] = t * slots + top_k;
-      if (lane == 0) nj = T;
-    } else {
-      int base = 0;
-      const int n = T * top_k;
-      for (int i0 = 0; i0 < n; i0 += 64) {
-        const int i = i0 + lane;
-        const bool m = i < n && idx[i] == e;
-        const unsigned long long mask = __ballot(m);
-        const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
-        if (m && pos < MOE_MAX_JOBS) jobs[pos] = (i / top_k) * slots + i % top_k;
-        base += __popcll(mask);
+// ---- schedule ---------------------------------------------------------------------
+//
+// Work items are (expert, 64-row tile, chunk of up to MOE_JPW jobs), the
+// shared expert being expert n_exp with every token's slot top_k.  Every
+// workgroup derives the same schedule from top_idx in LDS: jobs per expert
+// (LDS atomics: counts do not depend on order), exclusive sums of the
+// per-expert chunk and job counts (one wave), then the jobs bucketed by
+// expert in ascending slot order -- a slot's place is the number of earlier
+// slots routed to the same expert, so all workgroups agree on which jobs form
+// each chunk.  Items are numbered expert-major, then tile, then chunk, so the
+// chunks that share an expert tile are adjacent and run close together in
+// time (their weights are read from HBM about once).
+constexpr int MOE_JPW = 4;
+
+struct MoeSched {
+  int idx[MOE_MAX_JOBS];       // top_idx, flat
+  int fill[MOE_MAX_EXP + 1];   // jobs per expert
+  int coff[MOE_MAX_EXP + 2];   // exclusive sum of chunks per expert
+  int joff[MOE_MAX_EXP + 2];   // exclusive sum of jobs per expert
+  int jobs[2 * MOE_MAX_JOBS];  // t * slots + k, bucketed by expert, ascending
+};
+
+// Returns the number of chunks (items per tile).
+__device__ int moe_schedule(const int* __restrict__ idx, int T, int top_k, int n_exp, MoeSched& S) {
+  const int n = T * top_k, ne = n_exp + 1, slots = top_k + 1;
+  const int tid = threadIdx.x, bs = blockDim.x;
+  for (int i = tid; i < ne; i += bs) S.fill[i] = i == n_exp ? T : 0;
+  for (int i = tid; i < n; i += bs) S.idx[i] = idx[i];
+  __syncthreads();
+  for (int i = tid; i < n; i += bs) {
+    const int e = S.idx[i];
+    if (e >= 0 && e < n_exp) atomicAdd(&S.fill[e], 1);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int lane = tid;
+    int run_c = 0, run_j = 0;
+    for (int base = 0; base < ne; base += 64) {
+      const int e = base + lane;
+      const int c = e < ne ? S.fill[e] : 0;
+      const int ch = wave_scan_add((c + MOE_JPW - 1) / MOE_JPW), jc = wave_scan_add(c);  // inclusive
+      if (e < ne) {
+        S.coff[e] = run_c + ch - (c + MOE_JPW - 1) / MOE_JPW;
+        S.joff[e] = run_j + jc - c;
       }
-      if (lane == 0) nj = base < MOE_MAX_JOBS ? base : MOE_MAX_JOBS;
+      run_c += __builtin_amdgcn_readlane(ch, 63);
+      run_j += __builtin_amdgcn_readlane(jc, 63);
+    }
+    if (lane == 0) {
+      S.coff[ne] = run_c;
+      S.joff[ne] = run_j;
     }
   }
   __syncthreads();
-  return nj;
+  for (int i = tid; i < n; i += bs) {
+    const int e = S.idx[i];
+    if (e >= 0 && e < n_exp) {
+      int rank = 0;
+      for (int q = 0; q < i; ++q) rank += S.idx[q] == e;
+      S.jobs[S.joff[e] + rank] = (i / top_k) * slots + i % top_k;
+    }
+  }
+  for (int t = tid; t < T; t += bs) S.jobs[S.joff[n_exp] + t] = t * slots + top_k;
+  __syncthreads();
+  return S.coff[ne];
 }
 
-// Wave w of NW owns super-block columns w, w + NW, ..., (cpw of them); its
-// partial sums over them are accumulated in LDS and the NW partials of a
-// row summed in ascending wave order.  With cpw == 1 the weights stay in
-// registers for all of the expert's jobs; otherwise every pass of
-// MOE_JOBS_PER_PASS jobs reloads its columns (from L2 after the first pass).
+struct MoeItem {
+  int e, tile, j0, nj;  // expert, tile, first job (into S.jobs), job count
+};
+
+__device__ __forceinline__ MoeItem moe_item(const MoeSched& S, int ne, int tiles, int i) {
+  int lo = 0, hi = ne - 1;  // the expert e with coff[e] * tiles <= i < coff[e + 1] * tiles
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (S.coff[mid] * tiles <= i) lo = mid;
+    else hi = mid - 1;
+  }
+  const int e = lo, ch = S.coff[e + 1] - S.coff[e], r = i - S.coff[e] * tiles;
+  const int c = r % ch, cnt = S.joff[e + 1] - S.joff[e];
+  MoeItem it;
+  it.e = e;
+  it.tile = r / ch;
+  it.j0 = S.joff[e] + c * MOE_JPW;
+  it.nj = cnt - c * MOE_JPW < MOE_JPW ? cnt - c * MOE_JPW : MOE_JPW;
+  return it;
+}
+
+// ---- kernels ------------------------------------------------------------------------
+//
+// Wave w of NW owns super-block columns w, w + NW, ... (cpw of them) of the
+// item's tile; its partial sums over them are accumulated in LDS and the NW
+// partials of a row summed in ascending wave order.
+
+// Two workgroups per CU (four waves per SIMD at NW = 8), so one's weight
+// loads overlap the other's arithmetic -- for the kinds whose gate and up
+// registers fit in 128 VGPRs without spilling.
+constexpr int moe_gu_waves(int kind, int nw) {
+  return (kind == Q6_K || kind == Q8_0 || nw < 4) ? 1 : nw / 2;
+}
+
 template <int KIND, int NW>
-__global__ __launch_bounds__(64 * NW) void moe_gate_up(MoeGroupedArgs a, int cpw, const float* __restrict__ x,
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_waves(KIND, NW)))) void moe_gate_up(MoeGroupedArgs a, int cpw, const float* __restrict__ x,
                                                       float* __restrict__ h) {
-  __shared__ int jobs[MOE_MAX_JOBS];
-  __shared__ float part[MOE_JOBS_PER_PASS][NW][2][64];
+  __shared__ MoeSched S;
+  __shared__ float part[MOE_JPW][NW][2][64];
+  __shared__ __attribute__((aligned(16))) float xst[NW][256];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int e = blockIdx.x, tile = blockIdx.y;
-  const bool shared = e == a.n_exp;
-  const int slots = a.top_k + 1;
-  if (shared && tile == 0) {
+  const int slots = a.top_k + 1, ne = a.n_exp + 1, tiles = a.I / 64;
+  // Housekeeping for the down launch: zero its arrival counters, and the
+  // shared-expert gate g_t = sigmoid(shared_gate_inp . x_t) (one wave per token).
+  if (blockIdx.x == 0)
     for (int i = threadIdx.x; i < a.T * a.tiles_dim; i += blockDim.x) a.count[(size_t)i * COUNTER_STRIDE] = 0u;
-    if (w == 0)
-      for (int t = 0; t < a.T; ++t) {
-        float s = 0.f;
-        if (a.sgi)
-          for (int d = lane; d < a.dim; d += 64) s = __builtin_fmaf(a.sgi[d], x[(size_t)t * a.dim + d], s);
-        s = wave_sum(s);
-        if (lane == 0) a.gsh[t] = a.sgi ? 1.0f / (1.0f + expf(-s)) : 1.0f;
+  for (int t = blockIdx.x * NW + w; t < a.T; t += gridDim.x * NW) {
+    float s = 0.f;
+    if (a.sgi) {
+      // dim / 256 float4 per lane, loaded together (dim is a multiple of 256).
+      const float4* g4 = reinterpret_cast<const float4*>(a.sgi) + lane;
+      const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)t * a.dim) + lane;
+      for (int b = 0; b < a.dim / 4; b += 64 * 8) {
+        float4 gv[8], xv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int i = b + 64 * r < a.dim / 4 ? b + 64 * r : 0;
+          gv[r] = g4[i];
+          xv[r] = x4[i];
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (b + 64 * r < a.dim / 4) {
+            s = __builtin_fmaf(gv[r].x, xv[r].x, s);
+            s = __builtin_fmaf(gv[r].y, xv[r].y, s);
+            s = __builtin_fmaf(gv[r].z, xv[r].z, s);
+            s = __builtin_fmaf(gv[r].w, xv[r].w, s);
+          }
       }
+      s = wave_total(s);
+    }
+    if (lane == 0) a.gsh[t] = a.sgi ? 1.0f / (1.0f + expf(-s)) : 1.0f;
   }
-  const int nj = moe_jobs(a.idx, a.T, a.top_k, a.n_exp, e, jobs);
-  if (nj == 0) return;  // uniform over the workgroup
+  const int items = moe_schedule(a.idx, a.T, a.top_k, a.n_exp, S) * tiles;
   constexpr int GB = 64 * Block<KIND>::BYTES;
   const size_t nsb = (size_t)NW * cpw;
-  const uint8_t* G = (shared ? a.sh_gate : a.gate + (size_t)e * a.gu_stride) + (size_t)tile * nsb * GB;
-  const uint8_t* U = (shared ? a.sh_up : a.up + (size_t)e * a.gu_stride) + (size_t)tile * nsb * GB;
-  typename Packed<KIND>::R rg = Packed<KIND>::load(G + (size_t)w * GB, lane);
-  typename Packed<KIND>::R ru = Packed<KIND>::load(U + (size_t)w * GB, lane);
-  const int row = tile * 64 + lane;
-  for (int j0 = 0; j0 < nj; j0 += MOE_JOBS_PER_PASS) {
-    const int n = nj - j0 < MOE_JOBS_PER_PASS ? nj - j0 : MOE_JOBS_PER_PASS;
-    for (int j = 0; j < n; ++j) part[j][w][0][lane] = part[j][w][1][lane] = 0.f;  // this wave's slots only
+  for (int i = blockIdx.x; i < items; i += gridDim.x) {
+    const MoeItem it = moe_item(S, ne, tiles, i);
+    const bool shared = it.e == a.n_exp;
+    const uint8_t* G = (shared ? a.sh_gate : a.gate + (size_t)it.e * a.gu_stride) + (size_t)it.tile * nsb * GB;
+    const uint8_t* U = (shared ? a.sh_up : a.up + (size_t)it.e * a.gu_stride) + (size_t)it.tile * nsb * GB;
+    for (int j = 0; j < it.nj; ++j) part[j][w][0][lane] = part[j][w][1][lane] = 0.f;  // this wave's slots only
     for (int c = 0; c < cpw; ++c) {
       const int col = w + c * NW;
-      if (cpw > 1 && (c > 0 || j0 > 0)) {
-        rg = Packed<KIND>::load(G + (size_t)col * GB, lane);
-        ru = Packed<KIND>::load(U + (size_t)col * GB, lane);
-      }
+      const float4* xc = reinterpret_cast<const float4*>(x + (size_t)col * 256) + lane;
+      float4 xv = xc[(size_t)(S.jobs[it.j0] / slots) * (a.dim / 4)];
+      typename Packed<KIND>::R rg = Packed<KIND>::load(G + (size_t)col * GB, lane);
+      typename Packed<KIND>::R ru = Packed<KIND>::load(U + (size_t)col * GB, lane);
 #pragma unroll 1
-      for (int j = 0; j < n; ++j) {
-        // The job index is the same in every lane: say so, so that x is read
-        // with scalar loads into SGPRs rather than once per lane.
-        const int t = __builtin_amdgcn_readfirstlane(jobs[j0 + j]) / slots;
+      for (int j = 0; j < it.nj; ++j) {
+        const float4 cur = xv;
+        if (j + 1 < it.nj) xv = xc[(size_t)(S.jobs[it.j0 + j + 1] / slots) * (a.dim / 4)];  // next job's slice
+        float s16[16];
+        moe_stage(cur, xst[w], lane, s16);
         opaque_regs(rg);
         opaque_regs(ru);
-        const float2 gu = moe_sb_dot2<KIND>(rg, ru, x + (size_t)t * a.dim + (size_t)col * 256, lane);
+        const float2 gu = moe_dot2<KIND>(rg, ru, xst[w], s16);
         part[j][w][0][lane] += gu.x;
         part[j][w][1][lane] += gu.y;
       }
     }
     __syncthreads();
-    for (int j = w; j < n; j += NW) {
+    const int row = it.tile * 64 + lane;
+    for (int j = w; j < it.nj; j += NW) {
       float g = 0.f, u = 0.f;
 #pragma unroll
       for (int k = 0; k < NW; ++k) {
         g += part[j][k][0][lane];
         u += part[j][k][1][lane];
       }
-      if (row < a.I) h[(size_t)jobs[j0 + j] * a.I + row] = (g / (1.0f + expf(-g))) * u;
+      h[(size_t)S.jobs[it.j0 + j] * a.I + row] = (g / (1.0f + expf(-g))) * u;
     }
     __syncthreads();
   }
@@ -183,55 +269,57 @@ __global__ __launch_bounds__(64 * NW) void moe_gate_up(MoeGroupedArgs a, int cpw
 template <int KIND, int NW>
 __global__ __launch_bounds__(64 * NW) void moe_down(MoeGroupedArgs a, int cpw, const float* __restrict__ h,
                                                    float* __restrict__ yk, float* __restrict__ y) {
-  __shared__ int jobs[MOE_MAX_JOBS];
-  __shared__ float part[MOE_JOBS_PER_PASS][NW][64];
-  __shared__ int last[MOE_JOBS_PER_PASS];
+  __shared__ MoeSched S;
+  __shared__ float part[MOE_JPW][NW][64];
+  __shared__ __attribute__((aligned(16))) float xst[NW][256];
+  __shared__ int last[MOE_JPW];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int e = blockIdx.x, tile = blockIdx.y;
-  const bool shared = e == a.n_exp;
-  const int slots = a.top_k + 1;
-  const int nj = moe_jobs(a.idx, a.T, a.top_k, a.n_exp, e, jobs);
-  if (nj == 0) return;
+  const int slots = a.top_k + 1, ne = a.n_exp + 1, tiles = a.tiles_dim;
+  const int items = moe_schedule(a.idx, a.T, a.top_k, a.n_exp, S) * tiles;
   constexpr int GB = 64 * Block<KIND>::BYTES;
   const size_t nsb = (size_t)NW * cpw;
-  const uint8_t* D = (shared ? a.sh_down : a.down + (size_t)e * a.d_stride) + (size_t)tile * nsb * GB;
-  typename Packed<KIND>::R rd = Packed<KIND>::load(D + (size_t)w * GB, lane);
-  const int row = tile * 64 + lane;
-  for (int j0 = 0; j0 < nj; j0 += MOE_JOBS_PER_PASS) {
-    const int n = nj - j0 < MOE_JOBS_PER_PASS ? nj - j0 : MOE_JOBS_PER_PASS;
-    for (int j = 0; j < n; ++j) part[j][w][lane] = 0.f;  // this wave's slots only
+  for (int i = blockIdx.x; i < items; i += gridDim.x) {
+    const MoeItem it = moe_item(S, ne, tiles, i);
+    const bool shared = it.e == a.n_exp;
+    const uint8_t* D = (shared ? a.sh_down : a.down + (size_t)it.e * a.d_stride) + (size_t)it.tile * nsb * GB;
+    for (int j = 0; j < it.nj; ++j) part[j][w][lane] = 0.f;  // this wave's slots only
     for (int c = 0; c < cpw; ++c) {
       const int col = w + c * NW;
-      if (cpw > 1 && (c > 0 || j0 > 0)) rd = Packed<KIND>::load(D + (size_t)col * GB, lane);
+      const float4* hc = reinterpret_cast<const float4*>(h + (size_t)col * 256) + lane;
+      float4 hv = hc[(size_t)S.jobs[it.j0] * (a.I / 4)];
+      typename Packed<KIND>::R rd = Packed<KIND>::load(D + (size_t)col * GB, lane);
 #pragma unroll 1
-      for (int j = 0; j < n; ++j) {
-        const int job = __builtin_amdgcn_readfirstlane(jobs[j0 + j]);  // uniform: scalar loads of h
+      for (int j = 0; j < it.nj; ++j) {
+        const float4 cur = hv;
+        if (j + 1 < it.nj) hv = hc[(size_t)S.jobs[it.j0 + j + 1] * (a.I / 4)];  // next job's slice
+        float s16[16];
+        moe_stage(cur, xst[w], lane, s16);
         opaque_regs(rd);
-        const float v = moe_sb_dot<KIND>(rd, h + (size_t)job * a.I + (size_t)col * 256, lane);
-        part[j][w][lane] += v;
+        part[j][w][lane] += moe_dot<KIND>(rd, xst[w], s16);
       }
     }
     __syncthreads();
     // yk of each job (device-scope stores: the combine may run on another XCD).
-    for (int j = w; j < n; j += NW) {
+    const int row = it.tile * 64 + lane;
+    for (int j = w; j < it.nj; j += NW) {
       float v = 0.f;
 #pragma unroll
       for (int k = 0; k < NW; ++k) v += part[j][k][lane];
-      __hip_atomic_store(&yk[(size_t)jobs[j0 + j] * a.dim + row], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&yk[(size_t)S.jobs[it.j0 + j] * a.dim + row], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x < n) {
-      const int t = jobs[j0 + threadIdx.x] / slots;
-      last[threadIdx.x] = __hip_atomic_fetch_add(&a.count[((size_t)t * a.tiles_dim + tile) * COUNTER_STRIDE], 1u,
+    if (threadIdx.x < it.nj) {
+      const int t = S.jobs[it.j0 + threadIdx.x] / slots;
+      last[threadIdx.x] = __hip_atomic_fetch_add(&a.count[((size_t)t * tiles + it.tile) * COUNTER_STRIDE], 1u,
                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(slots - 1);
     }
     __syncthreads();
     // Combine every token whose last slot arrived here.
-    for (int j = w; j < n; j += NW)
+    for (int j = w; j < it.nj; j += NW)
       if (last[j]) {
-        const int t = jobs[j0 + j] / slots;
+        const int t = S.jobs[it.j0 + j] / slots;
         const float* yt = yk + (size_t)t * slots * a.dim + row;
         float acc = 0.f;
         for (int k = 0; k < a.top_k; ++k)
@@ -281,29 +369,62 @@ static int moe_waves(int nsb) {
   return 1;
 }
 
+// Workgroups of a launch: enough for every item the schedule can produce
+// (chunks <= jobs / MOE_JPW + non-empty experts), at most what the device
+// keeps resident at once; the kernels loop over items beyond the grid, so
+// no workgroup waits for a slot only to build the schedule again.
+static int moe_resident(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find({kernel, dev});
+  if (it != cache.end()) return it->second;
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
+  return cache[{kernel, dev}] = per * cus;
+}
+
+static int moe_grid(const MoeGroupedArgs& a, int tiles, int cap) {
+  const long slots = a.top_k + 1;
+  const long nonempty = std::min<long>(a.n_exp, (long)a.T * a.top_k) + 1;
+  const long bound = (long)tiles * (((long)a.T * slots + MOE_JPW - 1) / MOE_JPW + nonempty);
+  return (int)std::max<long>(1, std::min<long>(bound, cap));
+}
+
 template <int KIND>
 static hipError_t launch_gate_up_kind(const MoeGroupedArgs& a, hipStream_t s) {
-  const dim3 grid(a.n_exp + 1, (a.I + 63) / 64);
   const int nsb = a.dim / 256, nw = moe_waves(nsb);
+#define KQ_GU(N)                                                                                        \
+  case N: {                                                                                             \
+    const dim3 grid(moe_grid(a, a.I / 64, moe_resident((const void*)moe_gate_up<KIND, N>, 64 * N)));    \
+    hipLaunchKernelGGL((moe_gate_up<KIND, N>), grid, dim3(64 * N), 0, s, a, nsb / N, a.x, a.h);        \
+    break;                                                                                              \
+  }
   switch (nw) {
-#define KQ_GU(N) case N: hipLaunchKernelGGL((moe_gate_up<KIND, N>), grid, dim3(64 * N), 0, s, a, nsb / N, a.x, a.h); break;
     KQ_GU(1) KQ_GU(2) KQ_GU(3) KQ_GU(4) KQ_GU(8)
-#undef KQ_GU
     default: return hipErrorNotSupported;
   }
+#undef KQ_GU
   return hipGetLastError();
 }
 
 template <int KIND>
 static hipError_t launch_down_kind(const MoeGroupedArgs& a, hipStream_t s) {
-  const dim3 grid(a.n_exp + 1, a.tiles_dim);
   const int nsb = a.I / 256, nw = moe_waves(nsb);
+#define KQ_DN(N)                                                                                        \
+  case N: {                                                                                             \
+    const dim3 grid(moe_grid(a, a.tiles_dim, moe_resident((const void*)moe_down<KIND, N>, 64 * N)));    \
+    hipLaunchKernelGGL((moe_down<KIND, N>), grid, dim3(64 * N), 0, s, a, nsb / N, a.h, a.yk, a.y);     \
+    break;                                                                                              \
+  }
   switch (nw) {
-#define KQ_DN(N) case N: hipLaunchKernelGGL((moe_down<KIND, N>), grid, dim3(64 * N), 0, s, a, nsb / N, a.h, a.yk, a.y); break;
     KQ_DN(1) KQ_DN(2) KQ_DN(3) KQ_DN(4) KQ_DN(8)
-#undef KQ_DN
     default: return hipErrorNotSupported;
   }
+#undef KQ_DN
   return hipGetLastError();
 }
 
@@ -311,6 +432,8 @@ bool moe_grouped_supported(int dim, int I, int T, int top_k) {
   return dim > 0 && I > 0 && dim % 256 == 0 && I % 256 == 0 && T > 0 && top_k > 0 && top_k <= MOE_MAX_TOPK &&
          (size_t)T * top_k <= MOE_MAX_JOBS && T <= MOE_MAX_JOBS;
 }
+
+bool moe_grouped_experts_ok(int n_exp) { return n_exp > 0 && n_exp <= MOE_MAX_EXP; }
 
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s) {
   hipError_t e;

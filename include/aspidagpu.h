@@ -156,7 +156,9 @@ int aspida_dense_matvec_dev(const float *w, int in_dim, int out_dim, const float
  * [n_exp][dim]), stable softmax, greedy top-k (strict >, lowest index wins
  * ties), renormalised weights (src/llm/llm_moe.adb:136-197).  Writes
  * logits[T][n_exp], top_idx[T][top_k] (0-based) and top_w[T][top_k].
- * n_exp <= 1024, top_k <= 32, dim % 4 == 0. */
+ * n_exp <= 1024, top_k <= 32, dim % 4 == 0, router_w and x 16-byte aligned.
+ * Uses the stream's workspace like aspida_kq_matvec_packed_dev (allocated on
+ * the first call for a stream and T, so warm up before graph capture). */
 int aspida_moe_route_dev(const float *router_w, int n_exp, int dim, int T, int top_k, const float *x,
                          float *logits, int *top_idx, float *top_w, void *stream);
 
