@@ -73,6 +73,11 @@ def load(path=None):
         "aspida_moe_packed_work_bytes": (LG, [I, I, I, I]),
         "aspida_moe_pack_experts_dev": (I, [I, P, LG, I, I, I, P, P]),
         "aspida_moe_experts_packed_dev": (I, [P, I, I, I, I, I, P, P, P, P, I, P, I, P, P, P, P, P, P, P]),
+        "aspida_kq_chain_create": (P, [P, I]),
+        "aspida_kq_chain_run": (I, [P, P]),
+        "aspida_kq_chain_check": (I, [P]),
+        "aspida_kq_chain_workgroups": (I, [P]),
+        "aspida_kq_chain_destroy": (None, [P]),
         "aspida_kq_set_mv_config": (I, [I, I]),
     }
     for name, (res, args) in sig.items():
@@ -241,5 +246,54 @@ class DeviceOps:
                                                         shared_gate_inp or 0, work, y, stream),
                  "aspida_moe_experts_packed_dev")
 
+    def chain(self, steps):
+        """A resident decode chain over steps [(kind, packed_ptr, in_dim, out_dim, x_ptr, y_ptr), ...]."""
+        return Chain(self.lib, steps)
+
     def set_mv_config(self, rows_per_wave=0, waves_per_cu=16):
         self._ok(self.lib.aspida_kq_set_mv_config(rows_per_wave, waves_per_cu), "aspida_kq_set_mv_config")
+
+
+class KqStep(ctypes.Structure):
+    """aspida_kq_step (include/aspidagpu.h)."""
+    _fields_ = [("kind", ctypes.c_int), ("in_dim", ctypes.c_int), ("out_dim", ctypes.c_int),
+                ("reserved", ctypes.c_int), ("packed", ctypes.c_void_p), ("x", ctypes.c_void_p),
+                ("y", ctypes.c_void_p)]
+
+
+class Chain:
+    """aspida_kq_chain_*: create on construction, run(stream), check(), close()."""
+
+    def __init__(self, lib, steps):
+        self.lib = lib
+        arr = (KqStep * len(steps))(*[KqStep(k, i, o, 0, p, x, y) for k, p, i, o, x, y in steps])
+        self.h = lib.aspida_kq_chain_create(arr, len(steps))
+        if not self.h:
+            raise RuntimeError(f"aspida_kq_chain_create failed (error {lib.aspida_gpu_last_error()})")
+
+    def run(self, stream=0):
+        rc = self.lib.aspida_kq_chain_run(self.h, stream)
+        if rc:
+            raise RuntimeError(f"aspida_kq_chain_run: error {rc}")
+
+    def check(self):
+        """True when every dependency wait since the last check completed."""
+        rc = self.lib.aspida_kq_chain_check(self.h)
+        if rc < 0:
+            raise RuntimeError(f"aspida_kq_chain_check: error {rc}")
+        return rc == 0
+
+    def workgroups(self):
+        return int(self.lib.aspida_kq_chain_workgroups(self.h))
+
+    def close(self):
+        if self.h:
+            self.lib.aspida_kq_chain_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+

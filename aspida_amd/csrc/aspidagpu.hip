@@ -21,11 +21,13 @@
 #include <cstdint>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/aspidagpu.h"
 #include "kq_common.h"
 #include "kq_kernels.h"
 #include "kq_moe.h"
+#include "kq_chain.h"
 
 namespace {
 
@@ -734,6 +736,47 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
   }
   return 0;
 }
+
+extern "C" void* aspida_kq_chain_create(const aspida_kq_step* steps, int nsteps) {
+  if (!steps || nsteps <= 0) {
+    report(-EINVAL, "aspida_kq_chain_create: no steps");
+    return nullptr;
+  }
+  std::vector<kq::ChainStepDesc> d((size_t)nsteps);
+  for (int i = 0; i < nsteps; ++i) {
+    if (!valid_kind(steps[i].kind)) {
+      report(-EINVAL, "aspida_kq_chain_create: step %d: bad kind %d", i, steps[i].kind);
+      return nullptr;
+    }
+    d[i] = {steps[i].kind, steps[i].in_dim, steps[i].out_dim, steps[i].packed, steps[i].x, steps[i].y};
+  }
+  kq::Chain* c = nullptr;
+  const char* why = "";
+  const hipError_t e = kq::chain_create(d.data(), nsteps, &c, &why);
+  if (e != hipSuccess) {
+    report((int)e, "aspida_kq_chain_create: %s (%s)", why, hipGetErrorString(e));
+    return nullptr;
+  }
+  return c;
+}
+
+extern "C" int aspida_kq_chain_run(void* chain, void* stream) {
+  if (!chain) return -EINVAL;
+  return check(kq::chain_run((kq::Chain*)chain, (hipStream_t)stream), "aspida_kq_chain_run");
+}
+
+extern "C" int aspida_kq_chain_check(void* chain) {
+  if (!chain) return -EINVAL;
+  unsigned failed = 0;
+  const int rc = check(kq::chain_check((kq::Chain*)chain, &failed), "aspida_kq_chain_check");
+  return rc ? rc : (failed ? 1 : 0);
+}
+
+extern "C" int aspida_kq_chain_workgroups(void* chain) {
+  return chain ? kq::chain_workgroups((kq::Chain*)chain) : -EINVAL;
+}
+
+extern "C" void aspida_kq_chain_destroy(void* chain) { kq::chain_destroy((kq::Chain*)chain); }
 
 extern "C" int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu) {
   if (rows_per_wave > 0 && !(rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4)) return -EINVAL;

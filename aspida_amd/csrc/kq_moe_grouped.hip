@@ -33,55 +33,6 @@
 namespace kq {
 
 
-// Each wave multiplies its weight column by one job's 256 activations at a
-// time.  The lane's float4 of them is loaded from HBM/L2 one job ahead,
-// written to the wave's own LDS slot and read back by every lane (broadcast),
-// so a job costs one short LDS round trip instead of a chain of dependent
-// global loads.  Within a wave, LDS operations complete in program order, so
-// the slot needs no workgroup barrier; wave_barrier keeps the compiler from
-// moving the reads above the write.
-__device__ __forceinline__ void moe_stage(float4 v, float* __restrict__ slot, int lane, float (&s16)[16]) {
-  __builtin_amdgcn_wave_barrier();
-  *reinterpret_cast<float4*>(slot + 4 * lane) = v;
-  float t = (v.x + v.y) + (v.z + v.w);
-  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, false));
-  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, false));
-#pragma unroll
-  for (int j = 0; j < 16; ++j)
-    s16[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 4 * j));
-  __builtin_amdgcn_wave_barrier();
-}
-
-template <int KIND>
-__device__ __forceinline__ float moe_dot(const typename Packed<KIND>::R& r, const float* __restrict__ xs,
-                                         const float (&s16)[16]) {
-  using B = Block<KIND>;
-  float acc = 0.f;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    XQuarter X;
-    B::load_x(xs, s16, q, X);
-    acc += B::dot(Packed<KIND>::quarter(r, q), q, X);
-  }
-  return acc;
-}
-
-// The gate and up dots over the same staged activations.
-template <int KIND>
-__device__ __forceinline__ float2 moe_dot2(const typename Packed<KIND>::R& rg, const typename Packed<KIND>::R& ru,
-                                           const float* __restrict__ xs, const float (&s16)[16]) {
-  using B = Block<KIND>;
-  float g = 0.f, u = 0.f;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    XQuarter X;
-    B::load_x(xs, s16, q, X);
-    g += B::dot(Packed<KIND>::quarter(rg, q), q, X);
-    u += B::dot(Packed<KIND>::quarter(ru, q), q, X);
-  }
-  return make_float2(g, u);
-}
-
 // ---- schedule ---------------------------------------------------------------------
 //
 // Work items are (expert, 64-row tile, chunk of up to MOE_JPW jobs), the
@@ -243,10 +194,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_
         const float4 cur = xv;
         if (j + 1 < it.nj) xv = xc[(size_t)(S.jobs[it.j0 + j + 1] / slots) * (a.dim / 4)];  // next job's slice
         float s16[16];
-        moe_stage(cur, xst[w], lane, s16);
+        stage_x256(cur, xst[w], lane, s16);
         opaque_regs(rg);
         opaque_regs(ru);
-        const float2 gu = moe_dot2<KIND>(rg, ru, xst[w], s16);
+        const float2 gu = staged_dot2<KIND>(rg, ru, xst[w], s16);
         part[j][w][0][lane] += gu.x;
         part[j][w][1][lane] += gu.y;
       }
@@ -294,9 +245,9 @@ __global__ __launch_bounds__(64 * NW) void moe_down(MoeGroupedArgs a, int cpw, c
         const float4 cur = hv;
         if (j + 1 < it.nj) hv = hc[(size_t)S.jobs[it.j0 + j + 1] * (a.I / 4)];  // next job's slice
         float s16[16];
-        moe_stage(cur, xst[w], lane, s16);
+        stage_x256(cur, xst[w], lane, s16);
         opaque_regs(rd);
-        part[j][w][lane] += moe_dot<KIND>(rd, xst[w], s16);
+        part[j][w][lane] += staged_dot<KIND>(rd, xst[w], s16);
       }
     }
     __syncthreads();

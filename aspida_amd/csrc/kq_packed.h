@@ -161,4 +161,56 @@ template <> struct Packed<Q8_0> {
   }
 };
 
+#ifndef KQ_HOST_EMULATION
+// Activations staged through LDS: a wave that multiplies its super-block
+// column by a 256-element activation slice loads the slice as one float4 per
+// lane (a single coalesced 1 KB load, which can be issued well ahead), writes
+// it to the wave's own LDS slot and reads it back in every lane (broadcast),
+// instead of a chain of dependent scalar loads.  Within a wave, LDS
+// operations complete in program order, so the slot needs no workgroup
+// barrier; wave_barrier keeps the compiler from moving the reads above the
+// write.  The per-16 sums the K-quant dots take come from the same float4s.
+__device__ __forceinline__ void stage_x256(float4 v, float* __restrict__ slot, int lane, float (&s16)[16]) {
+  __builtin_amdgcn_wave_barrier();
+  *reinterpret_cast<float4*>(slot + 4 * lane) = v;
+  float t = (v.x + v.y) + (v.z + v.w);
+  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, false));
+  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, false));
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    s16[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 4 * j));
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int KIND>
+__device__ __forceinline__ float staged_dot(const typename Packed<KIND>::R& r, const float* __restrict__ xs,
+                                         const float (&s16)[16]) {
+  using B = Block<KIND>;
+  float acc = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    XQuarter X;
+    B::load_x(xs, s16, q, X);
+    acc += B::dot(Packed<KIND>::quarter(r, q), q, X);
+  }
+  return acc;
+}
+
+// The gate and up dots over the same staged activations.
+template <int KIND>
+__device__ __forceinline__ float2 staged_dot2(const typename Packed<KIND>::R& rg, const typename Packed<KIND>::R& ru,
+                                           const float* __restrict__ xs, const float (&s16)[16]) {
+  using B = Block<KIND>;
+  float g = 0.f, u = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    XQuarter X;
+    B::load_x(xs, s16, q, X);
+    g += B::dot(Packed<KIND>::quarter(rg, q), q, X);
+    u += B::dot(Packed<KIND>::quarter(ru, q), q, X);
+  }
+  return make_float2(g, u);
+}
+#endif  // KQ_HOST_EMULATION
+
 }  // namespace kq

@@ -90,6 +90,35 @@ class Decoder:
         self.y = {name: torch.empty(out, **f) for name, _, out, _, _ in layer_plan()}
         self.logits = torch.empty(VOCAB, **f)
 
+    def build_chain(self):
+        """The whole token as one resident chain (aspida_kq_chain_*): per layer
+        q|k and v read the layer input, o reads the q rows, gate|up reads o,
+        down reads the gate rows, and the next layer reads down -- each step's
+        input is the previous step's output, as in the decoder, with the
+        element-wise work between them left out (it streams no weights).
+        Outputs live in one arena, a vector per step and layer."""
+        torch = self.torch
+        plan = {name: (kind, out, inp) for name, kind, out, inp, _ in layer_plan()}
+        sizes = [("h", HIDDEN)] + [(f"{n}{l}", plan[n][1]) for l in range(LAYERS) for n in plan] + [("logits", VOCAB)]
+        off, n = {}, 0
+        for name, size in sizes:
+            off[name] = n
+            n += (size + 63) // 64 * 64
+        self.arena = torch.randn(n, device="cuda")
+        base = self.arena.data_ptr()
+        ptr = lambda name, start=0: base + 4 * (off[name] + start)
+        steps = []
+        for l, L in enumerate(self.layers):
+            xin = ptr("h") if l == 0 else ptr(f"down{l - 1}")
+            src = {"qk": xin, "v": xin, "o": ptr(f"qk{l}"), "gate_up": ptr(f"o{l}"), "down": ptr(f"gate_up{l}")}
+            for name in ("qk", "v", "o", "gate_up", "down"):
+                kind, out, inp = plan[name]
+                steps.append((kind, L[name].data_ptr(), inp, out, src[name], ptr(f"{name}{l}")))
+        steps.append((Q6_K, self.head.data_ptr(), HIDDEN, VOCAB, ptr(f"down{LAYERS - 1}"), ptr("logits")))
+        self.chain_steps = steps
+        self.chain = self.dev.chain(steps)
+        return self.chain
+
     def launches(self):
         """Per launch, in decode order: a tuple of (kind, packed_ptr, in, out, x_key, y_ptr), one entry per
         matrix of the launch."""
@@ -428,31 +457,46 @@ def main():
     dec = Decoder(torch, aa, synth, args.seed)
     torch.cuda.synchronize()
 
-    # Warm the path eagerly once (first-call set-up happens outside capture), then capture one token.
-    with torch.cuda.stream(stream):
-        dec.step(stream.cuda_stream)
-    stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        dec.step(stream.cuda_stream)
-    with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
-            graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        e0.record(stream)
-        for _ in range(args.steps):
-            graph.replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_s = e0.elapsed_time(e1) * 1e-3
+    def timed(step_fn, steps, warmup):
+        """Capture one token, replay `warmup` times, then time `steps` replays
+        (wall clock around synchronised replays, and HIP events on the stream)."""
+        with torch.cuda.stream(stream):
+            step_fn(stream.cuda_stream)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step_fn(stream.cuda_stream)
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(steps):
+                graph.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        del graph
+        return wall, e0.elapsed_time(e1) * 1e-3
+
+    # The token: per-matrix launches of the packed batch-1 kernels (q|k and v
+    # share one), captured in one HIP graph.
+    wall, gpu_s = timed(dec.step, args.steps, args.warmup)
     tok_s = args.steps / wall
-    print(f"# decode: {args.steps} tokens in {wall * 1e3:.1f} ms wall ({gpu_s * 1e3:.1f} ms events)",
-          file=sys.stderr, flush=True)
-    del graph
+    print(f"# decode (per-matrix launches): {args.steps} tokens in {wall * 1e3:.1f} ms wall "
+          f"({gpu_s * 1e3:.1f} ms events) = {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
+    # The same token as one resident-chain launch (aspida_kq_chain_*), reported beside it.
+    chain = dec.build_chain()
+    cwall, cgpu = timed(lambda sp: chain.run(sp), args.steps, args.warmup)
+    chain_ok = chain.check()
+    chain_info = {"tok_s": round(args.steps / cwall, 2), "ms_per_step": round(cwall * 1e3 / args.steps, 4),
+                  "gpu_event_ms_per_step": round(cgpu * 1e3 / args.steps, 4), "workgroups": chain.workgroups(),
+                  "waits_completed": bool(chain_ok)}
+    print(f"# decode (resident chain): {args.steps / cwall:.1f} tok/s", file=sys.stderr, flush=True)
+    chain.close()
 
     # Dominant kernel: per kernel, its launches of one step in a graph of their own, timed with events.
     groups = kernel_events(torch, dec, stream)
@@ -463,6 +507,7 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom_key),
                 "launches_per_step": dom["launches"], "avg_launch_us": dom["avg_us"],
                 "bytes_per_launch": dom["bytes"] // dom["launches"]}
+    stream_bytes = 4_875_853_824
     if args.copy_probe_mib:
         a = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda")
         b = torch.empty_like(a)
@@ -481,7 +526,6 @@ def main():
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         cpu = cpu_baseline(args.seed, threads)
 
-    stream_bytes = 4_875_853_824
     line = {
         "metric": "Llama-3-8B Q4_K_M decode weight stream tok/s (batch 1) + K-quant matvec HBM GB/s",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -495,6 +539,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": groups,
+        "resident_chain": chain_info,
         "kquant_matvec": table,
         "small_batch_mfma": small,
         "moe_layer": moe,

@@ -197,6 +197,38 @@ int aspida_moe_experts_packed_dev(const float *x, int T, int dim, int top_k, int
                                   const void *shg_p, const void *shu_p, const void *shd_p,
                                   const float *shared_gate_inp, void *work, float *y, void *stream);
 
+/* Resident decode chain: an ordered list of packed matvecs (steps) run by ONE
+ * persistent launch, with no launch boundary between them -- e.g. every
+ * weight matrix of a decoder pass.  A step whose x lies inside an earlier
+ * step's y (its producer: the latest earlier step whose y overlaps x; x must
+ * lie wholly inside it) waits, per 256-element column, only for the 64-row
+ * tiles of the producer that write those elements, while the weight loads
+ * of the following columns are already in flight; other steps read x as
+ * given.  No step may write memory that an earlier step reads or writes, or
+ * its own x.  Same arithmetic per row as aspida_kq_matvec_packed_dev (a
+ * different, fixed order of the per-column sums; deterministic).  No
+ * counterpart in the reference, whose per-call ABI this path replaces for
+ * callers that keep weights and activations in HBM
+ * (aspida_gpu_matvec, gpu/gpu_matvec.cu:502-530, called per matrix).
+ * aspida_kq_chain_create validates the steps and allocates the chain's
+ * flags and partial sums (NULL on error, see aspida_gpu_last_error);
+ * aspida_kq_chain_run launches it on `stream` and allocates nothing (runs of
+ * one chain must be ordered); aspida_kq_chain_check synchronises and returns
+ * 1 if a dependency wait gave up since the last check (outputs of that run
+ * unreliable; only when the device could not keep every workgroup
+ * resident), else 0; aspida_kq_chain_workgroups: the launch's workgroups. */
+typedef struct aspida_kq_step {
+  int kind, in_dim, out_dim, reserved;
+  const void *packed;   /* aspida_kq_pack_dev layout */
+  const float *x;       /* [in_dim], 16-byte aligned */
+  float *y;             /* [out_dim] */
+} aspida_kq_step;
+void *aspida_kq_chain_create(const aspida_kq_step *steps, int nsteps);
+int aspida_kq_chain_run(void *chain, void *stream);
+int aspida_kq_chain_check(void *chain);
+int aspida_kq_chain_workgroups(void *chain);
+void aspida_kq_chain_destroy(void *chain);
+
 /* Launch-shape override for batch-1 matvecs: rows per lane group per step
  * (1, 2 or 4) and resident waves launched per CU (1..64); rows_per_wave <= 0
  * restores the built-in choice.  Process-wide; for tuning and tests. */

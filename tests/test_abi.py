@@ -131,3 +131,24 @@ def test_grouped_moe_rejects_bad_arguments(lib):
     assert call(work=one + 16) < 0      # work must be 256-byte aligned
     assert lib.aspida_moe_pack_experts_dev(0, one, 10, 256, 64, 2, one, None) < 0   # stride below one matrix
     assert lib.aspida_moe_pack_experts_dev(0, one, 64 * 144, 300, 64, 2, one, None) < 0
+
+
+def test_chain_rejects_bad_steps(lib):
+    """aspida_kq_chain_create validates before allocating: a step that writes
+    what an earlier step reads, an input straddling a producer's output, an
+    unaligned x, a bad kind."""
+    def mk(steps):
+        arr = (aa.KqStep * len(steps))(*[aa.KqStep(k, i, o, 0, p, x, y) for k, p, i, o, x, y in steps])
+        return lib.aspida_kq_chain_create(arr, len(steps))
+    B = 1 << 20                         # fake device addresses, never dereferenced
+    ok0 = (0, 4096, 256, 64, B, B + 4096)
+    assert not mk([(0, 4096, 256, 64, B, B + 512)])                       # x overlaps its own y
+    assert not mk([ok0, (0, 4096, 256, 64, B + 8192, B)])                 # writes x of step 0
+    assert not mk([ok0, (0, 4096, 256, 64, B + 4096 + 128, B + 8192)])   # x straddles step 0's y
+    assert not mk([(0, 4096, 256, 64, B + 4, B + 4096)])                  # x not 16-byte aligned
+    assert not mk([(9, 4096, 256, 64, B, B + 4096)])                      # bad kind
+    assert not mk([(0, 4096, 300, 64, B, B + 4096)])                      # in_dim % 256
+    assert lib.aspida_gpu_last_error() != 0
+    assert lib.aspida_kq_chain_run(None, None) < 0
+    assert lib.aspida_kq_chain_check(None) < 0
+    lib.aspida_kq_chain_destroy(None)
