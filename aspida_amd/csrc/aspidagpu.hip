@@ -172,8 +172,8 @@ struct MvWorkspace {
   DevBuf<unsigned> count;
   DevBuf<uint8_t> mm;  // activation split and partials of the MFMA product
   int ensure(int in_dim, int out_dim, int batch = 1) {
-    if (part.ensure(std::max<size_t>(kq::packed_workspace_floats(in_dim, out_dim), 64), "hipMalloc partials"))
-      return -1;
+    const size_t pf = batch > 1 ? kq::multi_workspace_floats(in_dim, out_dim) : kq::packed_workspace_floats(in_dim, out_dim);
+    if (part.ensure(std::max<size_t>(pf, 64), "hipMalloc partials")) return -1;
     if (batch > 1 && mm.ensure(kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, 64)), "hipMalloc mfma"))
       return -1;
     const size_t want = kq::packed_counters(out_dim);
@@ -183,11 +183,17 @@ struct MvWorkspace {
   }
 };
 
-// Y[batch][out] = X W^T over packed W on `st`: MFMA kernels for the kinds that
-// have them (64 activation rows per launch), else one packed matvec per row.
+// Y[batch][out] = X W^T over packed W on `st`: small batches on the
+// multi-vector VALU kernel (up to 4 vectors for the kinds with MFMA kernels,
+// where MFMA is faster from 5 on; 8 per launch for the others), larger Q4_K /
+// Q6_K batches on MFMA (64 activation rows per launch).
+constexpr int MULTI_MAX_BATCH = 8;
+constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
                          MvWorkspace& ws, hipStream_t st) {
-  if (batch > 1 && kq::mfma_kind(kind)) {
+  if (batch == 1)
+    return kq::launch_matvec_packed(kind, P, in_dim, out_dim, X, Y, ws.part.p, ws.count.p, st);
+  if (batch > MULTI_MAX_BATCH_MFMA_KINDS && kq::mfma_kind(kind)) {
     for (int b0 = 0; b0 < batch; b0 += 64) {
       const int nb = std::min(64, batch - b0);
       const hipError_t e = kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, X + (size_t)b0 * in_dim,
@@ -196,9 +202,10 @@ hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int b
     }
     return hipSuccess;
   }
-  for (int b = 0; b < batch; ++b) {
-    const hipError_t e = kq::launch_matvec_packed(kind, P, in_dim, out_dim, X + (size_t)b * in_dim,
-                                                  Y + (size_t)b * out_dim, ws.part.p, ws.count.p, st);
+  for (int b0 = 0; b0 < batch; b0 += MULTI_MAX_BATCH) {
+    const int nb = std::min(MULTI_MAX_BATCH, batch - b0);
+    const hipError_t e = kq::launch_matmul_packed_valu(kind, P, in_dim, out_dim, nb, X + (size_t)b0 * in_dim,
+                                                       Y + (size_t)b0 * out_dim, ws.part.p, ws.count.p, st);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -310,24 +317,15 @@ extern "C" void aspida_gpu_matmul(const void* w, long wbytes, int kind, int in_d
     return;
   }
   Ctx& c = ctx();
-  int rc;
-  if (batch == 1 || kq::mfma_kind(kind)) {
-    // Packed HBM mirror (shared with aspida_gpu_matvec): MFMA for Q4_K / Q6_K.
-    void* dw = packed_weight(w, kind, in_dim, out_dim);
-    rc = dw ? 0 : -1;
-    if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim, batch) ? -1 : 0;
-    if (!rc)
-      rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, false, [&]() {
-        return matmul_packed(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.ws, c.st);
-      });
-  } else {
-    void* dw = weight(w, need_bytes(kind, in_dim, out_dim));
-    rc = dw ? 0 : -1;
-    if (!rc)
-      rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, true, [&]() {
-        return kq::launch_matmul_valu(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dq.p, c.dy.p, c.st);
-      });
-  }
+  // Packed HBM mirror (shared with aspida_gpu_matvec): the multi-vector VALU
+  // kernel up to 8 vectors at a time, MFMA for larger Q4_K / Q6_K batches.
+  void* dw = packed_weight(w, kind, in_dim, out_dim);
+  int rc = dw ? 0 : -1;
+  if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim, batch) ? -1 : 0;
+  if (!rc)
+    rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, false, [&]() {
+      return matmul_packed(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.ws, c.st);
+    });
   if (rc) fill_nan(y, (long)out_dim * batch);
 }
 

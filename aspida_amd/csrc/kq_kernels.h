@@ -74,6 +74,13 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
                                      float* Y, void* work, unsigned* count, hipStream_t s);
 
 // ggml layout -> packed (unpack = false) or back (unpack = true).
+// Y[b][out] = W X[b] for nb <= 8 vectors over packed W on VALU
+// (kq_packed_multi.hip); row b is bit-identical to launch_matvec_packed on
+// X[b].  part: multi_workspace_floats floats; count as for the matvec.
+size_t multi_workspace_floats(int in_dim, int out_dim);
+hipError_t launch_matmul_packed_valu(int kind, const void* P, int in_dim, int out_dim, int nb, const float* X, float* Y,
+                                     float* part, unsigned* count, hipStream_t s);
+
 hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void* dst, bool unpack, hipStream_t s);
 
 // y = W x for packed W; x is 16-byte aligned.  Launches that share a

@@ -162,6 +162,34 @@ template <> struct Packed<Q8_0> {
 };
 
 #ifndef KQ_HOST_EMULATION
+// s16[j] = sum of xs[16j .. 16j+15] for the 256 activations at xs (16-byte
+// aligned), as wave-uniform values.
+__device__ __forceinline__ void sb_sums(const float* __restrict__ xs, int lane, float (&s16)[16]) {
+  float4 v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(xs + 4 * lane, 16), 16);
+  float t = (v.x + v.y) + (v.z + v.w);
+  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0xB1, 0xF, 0xF, false));
+  t += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x4E, 0xF, 0xF, false));
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s16[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t), 4 * j));
+}
+
+// One super-block column of row `lane`: sum_i w_i x_i over its 256 elements.
+template <int KIND>
+__device__ __forceinline__ float sb_dot(const typename Packed<KIND>::R& r, const float* __restrict__ xs, int lane) {
+  using B = Block<KIND>;
+  float s16[16];
+  sb_sums(xs, lane, s16);
+  float acc = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    XQuarter X;
+    B::load_x(xs, s16, q, X);
+    acc += B::dot(Packed<KIND>::quarter(r, q), q, X);
+  }
+  return acc;
+}
+
 // Activations staged through LDS: a wave that multiplies its super-block
 // column by a 256-element activation slice loads the slice as one float4 per
 // lane (a single coalesced 1 KB load, which can be issued well ahead), writes

@@ -59,6 +59,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--only", choices=["small", "moe", "kquant"],
+                    help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
@@ -256,9 +258,10 @@ def kquant_table(torch, aa, synth, seed, stream):
 
 def small_batch_table(torch, aa, synth, seed, stream):
     """Small-batch products: Q4_K and Q6_K at 4096x4096 and
-    14336x4096 for B in {2, 4, 8, 16, 32, 64}, packed weights on the MFMA
-    kernels, launches rotating over >= 1 GiB of weight copies.  GB/s counts
-    W + 4 B (in + out) bytes; TFLOP/s counts 2 B in out."""
+    14336x4096 for B in {2, 4, 8, 16, 32, 64}, packed weights (the
+    multi-vector VALU kernel up to B = 4, MFMA above), launches rotating over
+    >= 1 GiB of weight copies.  GB/s counts W + 4 B (in + out) bytes;
+    TFLOP/s counts 2 B in out."""
     dev = aa.DeviceOps()
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 2)
@@ -295,6 +298,7 @@ def small_batch_table(torch, aa, synth, seed, stream):
                 t = e0.elapsed_time(e1) * 1e-3 / (3 * ncopy)
                 nbytes = aa.weight_bytes(kind, inp, out) + 4 * B * (inp + out)
                 table[f"{aa.KIND_NAMES[kind]} {out}x{inp} B={B}"] = {
+                    "kernel": "kq_mm_packed_valu" if B <= 4 else "kq_mm_mfma",
                     "us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
                     "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3),
                     "TFLOPs": round(2.0 * B * inp * out / t / 1e12, 2)}
@@ -454,6 +458,10 @@ def main():
         sys.exit(1)
     aa.load()                                       # fails loudly without the HIP library
     stream = torch.cuda.Stream()
+    if args.only:
+        fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
+        print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
+        return
     dec = Decoder(torch, aa, synth, args.seed)
     torch.cuda.synchronize()
 
@@ -541,7 +549,7 @@ def main():
         "kernels": groups,
         "resident_chain": chain_info,
         "kquant_matvec": table,
-        "small_batch_mfma": small,
+        "small_batch": small,
         "moe_layer": moe,
     }
     assert dec_bytes_ok(stream_bytes), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"

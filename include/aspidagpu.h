@@ -126,11 +126,14 @@ int aspida_kq_matvec2_packed_dev(int kind_a, const void *packed_a, int out_a, fl
                                  void *stream);
 
 /* Y[batch][out_dim] = X[batch][in_dim] W^T for packed W: the small-batch
- * path.  Q4_K and Q6_K run on MFMA (activations split into f16 hi + lo, exact
- * integer codes, f32 scales; 64 rows per launch); other kinds run the packed
- * matvec once per row.  x must be 16-byte aligned; workspace as for
- * aspida_kq_matvec_packed_dev.  The same math as the reference's batched
- * kernels (gpu/gpu_matvec.cu:234-382) without its batch limit of 32. */
+ * path.  Small batches run on a multi-vector VALU kernel, each row
+ * bit-identical to aspida_kq_matvec_packed_dev on it: up to 4 rows for Q4_K
+ * and Q6_K, whose larger batches run on MFMA (activations split into f16
+ * hi + lo, exact integer codes, f32 scales; 64 rows per launch), and 8 rows
+ * per launch for the other kinds.
+ * x must be 16-byte aligned; workspace as for aspida_kq_matvec_packed_dev.
+ * The same math as the reference's batched kernels (gpu/gpu_matvec.cu:234-382)
+ * without its batch limit of 32. */
 int aspida_kq_matmul_packed_dev(int kind, const void *packed, int in_dim, int out_dim, int batch,
                                 const float *x, float *y, void *stream);
 

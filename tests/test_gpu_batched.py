@@ -69,6 +69,62 @@ def _packed_matmul(kind, w, X, in_dim, out_dim):
     return dy.cpu().numpy()
 
 
+def _packed_rows(kind, w, X, in_dim, out_dim):
+    """The batch-1 packed matvec of every row of X (same packed image)."""
+    torch = torch_cuda()
+    dev = aa.DeviceOps()
+    dw = to_dev(w)
+    dp = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+    dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+    out = []
+    for b in range(X.shape[0]):
+        dx = to_dev(np.ascontiguousarray(X[b], np.float32))
+        dy = torch.full((out_dim,), float("nan"), device="cuda")
+        dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
+        sync()
+        out.append(dy.cpu().numpy())
+    return np.stack(out)
+
+
+# Multi-vector VALU product (up to 4 rows for Q4_K/Q6_K, 8 for the other
+# kinds; rows bit-identical to the batch-1 kernel): ragged weight rows, one
+# super-block column, tiles split over workgroups (ks > 1), columns per wave
+# > 1.  Q4_K/Q6_K batches of 5 and 8 go to MFMA and are checked row by row.
+MULTI_CASES = [(2, 130, 768), (3, 1000, 4096), (4, 64, 14336), (5, 64, 14336), (8, 300, 256), (8, 4096, 4096)]
+
+
+@pytest.mark.parametrize("case", MULTI_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
+@pytest.mark.parametrize("kind", list(aa.KINDS))
+def test_multi_vector_rows_bit_identical_to_matvec(kind, case):
+    batch, out_dim, in_dim = case
+    gen = synth.rng(700 + batch + kind * 7 + out_dim)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    if kind in (aa.Q4_K, aa.Q6_K) and batch > 4:
+        # served by the MFMA kernel: every row against the oracle instead
+        for b in range(batch):
+            want = oracle.qmatvec(kind, w, in_dim, out_dim, X[b], nthreads=ncpu())
+            assert_close_scaled(Y[b], want, abs_dot_scale(kind, w, in_dim, out_dim, X[b]), what=f"row {b}")
+        return
+    R = _packed_rows(kind, w, X, in_dim, out_dim)
+    assert np.array_equal(Y.view(np.uint32), R.view(np.uint32)), "rows differ from the batch-1 kernel"
+    want = oracle.qmatvec(kind, w, in_dim, out_dim, X[-1], nthreads=ncpu())
+    assert_close_scaled(Y[-1], want, abs_dot_scale(kind, w, in_dim, out_dim, X[-1]), what="last row")
+
+
+@pytest.mark.parametrize("kind", [aa.Q5_K, aa.Q8_0])
+def test_multi_vector_chunks_beyond_eight(kind):
+    """Kinds without MFMA run batches above 8 as launches of 8."""
+    batch, out_dim, in_dim = 19, 200, 512
+    gen = synth.rng(811 + kind)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    R = _packed_rows(kind, w, X, in_dim, out_dim)
+    assert np.array_equal(Y.view(np.uint32), R.view(np.uint32))
+
+
 # MFMA product (Q4_K, Q6_K): one and several 16-row activation blocks, ragged
 # batch sizes, more than 64 rows (two launches), ragged weight rows, one
 # workgroup per tile and tiles split over workgroups.
