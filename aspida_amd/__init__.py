@@ -78,6 +78,7 @@ def load(path=None):
         "aspida_kq_chain_check": (I, [P]),
         "aspida_kq_chain_workgroups": (I, [P]),
         "aspida_kq_chain_destroy": (None, [P]),
+        "aspida_kq_set_packed_plan": (I, [I, I]),
         "aspida_kq_set_mv_config": (I, [I, I]),
     }
     for name, (res, args) in sig.items():

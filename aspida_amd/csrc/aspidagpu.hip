@@ -776,6 +776,12 @@ extern "C" int aspida_kq_chain_workgroups(void* chain) {
 
 extern "C" void aspida_kq_chain_destroy(void* chain) { kq::chain_destroy((kq::Chain*)chain); }
 
+extern "C" int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile) {
+  if (waves_per_group < 0 || groups_per_tile < 0) return -EINVAL;
+  kq::set_packed_plan_override(waves_per_group, groups_per_tile);
+  return 0;
+}
+
 extern "C" int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu) {
   if (rows_per_wave > 0 && !(rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4)) return -EINVAL;
   if (rows_per_wave > 0 && (waves_per_cu < 1 || waves_per_cu > 64)) return -EINVAL;

@@ -44,6 +44,9 @@ struct PackedPlan {
   int nw, ks, spw;
 };
 PackedPlan packed_plan(int in_dim, int out_dim);
+// Process-wide override of packed_plan for tuning (nw a power of two <= 16,
+// nw * ks dividing in_dim / 256; anything else, or 0, restores the choice).
+void set_packed_plan_override(int nw, int ks);
 
 // Bytes of the packed image of a [out_dim][in_dim] matrix (rows rounded up to
 // a multiple of 64); 0 for an invalid kind or shape.

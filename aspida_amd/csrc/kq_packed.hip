@@ -18,6 +18,8 @@
 // memset.
 #include <algorithm>
 
+#include <atomic>
+
 #include "kq_packed.h"
 #include "kq_kernels.h"
 
@@ -195,19 +197,38 @@ size_t packed_bytes(int kind, int in_dim, int out_dim) {
 // workgroup of up to 16 waves covering a whole tile needs no cross-workgroup
 // sum, and is the fastest split whenever there are enough tiles to occupy
 // the chip: with >= 256 tiles the columns per wave are chosen for about 14
-// waves per CU, with >= 64 tiles and <= 16 columns every wave takes one
-// column.  Narrower matrices split each tile over ks workgroups of up to 8
-// waves (4 below 32 tiles, for more workgroups), one column per wave.
+// waves per CU, with 128..255 tiles and <= 16 columns every wave takes one
+// column.  Below 128 tiles of <= 16 columns a tile is spread over up to 8
+// workgroups (about 256 in all), and other narrow matrices split each tile
+// over ks workgroups of up to 8 waves (4 below 32 tiles), one column per wave.
 static int pow2_divisor_upto(int n, int cap) {
   int d = 1;
   while (d * 2 <= cap && n % (d * 2) == 0) d *= 2;
   return d;
 }
 
+// Process-wide override of the split (tuning): waves per workgroup and
+// workgroups per tile, 0 = the built-in choice.
+static std::atomic<int> g_plan_nw{0}, g_plan_ks{0};
+
+void set_packed_plan_override(int nw, int ks) {
+  g_plan_nw = nw;
+  g_plan_ks = ks;
+}
+
 PackedPlan packed_plan(int in_dim, int out_dim) {
   static const int cus = device_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   PackedPlan p{1, 1, nsb};
+  {
+    const int onw = g_plan_nw, oks = g_plan_ks;
+    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && onw <= 16 && nsb % (onw * oks) == 0) {
+      p.nw = onw;
+      p.ks = oks;
+      p.spw = nsb / (onw * oks);
+      return p;
+    }
+  }
   if (ntiles >= 256) {
     const double target = 14.0 * cus;
     double best = 1e30;
@@ -219,6 +240,17 @@ PackedPlan packed_plan(int in_dim, int out_dim) {
     }
     p.nw = pow2_divisor_upto(nsb / p.spw, 16);
     p.spw = nsb / p.nw;
+    return p;
+  }
+  if (nsb <= 16 && ntiles < 128) {
+    // Narrow and short (o, q|k, v of a decoder): spread each tile over up to
+    // 8 workgroups so that about 256 take part; measured on MI355X, 11% faster
+    // on 4096^2 than one workgroup per tile.
+    int want = 1;
+    while (want * 2 <= 8 && ntiles * want * 2 <= 256) want *= 2;
+    p.ks = pow2_divisor_upto(nsb, want);
+    p.nw = pow2_divisor_upto(nsb / p.ks, 16);
+    p.spw = nsb / (p.ks * p.nw);
     return p;
   }
   if (ntiles >= 64 && nsb <= 16) {

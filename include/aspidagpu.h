@@ -232,6 +232,12 @@ int aspida_kq_chain_check(void *chain);
 int aspida_kq_chain_workgroups(void *chain);
 void aspida_kq_chain_destroy(void *chain);
 
+/* Split override for the packed kernels (aspida_kq_packed_plan): waves per
+ * workgroup (a power of two <= 16) and workgroups per tile, applied to every
+ * shape whose in_dim / 256 they divide; 0, 0 restores the built-in choice.
+ * Process-wide; for tuning and tests. */
+int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile);
+
 /* Launch-shape override for batch-1 matvecs: rows per lane group per step
  * (1, 2 or 4) and resident waves launched per CU (1..64); rows_per_wave <= 0
  * restores the built-in choice.  Process-wide; for tuning and tests. */
