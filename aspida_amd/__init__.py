@@ -94,7 +94,9 @@ def exported_symbols_declared():
     """Function names declared in include/aspidagpu.h."""
     import re
     txt = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:void|int|long long|long)\s+(aspida_\w+)\s*\(", txt, re.M)))
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?!typedef\b)(?:const\s+)?[A-Za-z_]\w*(?:\s+\w+)*[\s\*]+(aspida_\w+)\s*\(",
+                                 txt, re.M)))
 
 
 def _p(a):

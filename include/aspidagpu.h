@@ -232,6 +232,40 @@ int aspida_kq_chain_check(void *chain);
 int aspida_kq_chain_workgroups(void *chain);
 void aspida_kq_chain_destroy(void *chain);
 
+/* ---- GGUF tensor layout (host only) ----------------------------------------
+ * A reader of GGUF model files for locating and checking real weights: the
+ * header, metadata and tensor descriptors with the reference loader's rules
+ * (LLM_GGUF.Open_From_Source, src/llm/llm_gguf.adb:317-560; byte sizes per
+ * Checked_Byte_Size, 238-258; type codes per To_GGML_Type, 266-291).  A
+ * tensor's kind is this library's code (0 Q4_K, 1 Q6_K, 2 Q5_K, 3 Q3_K,
+ * 4 Q2_K, 5 Q8_0; LLM_Weight.Kind_Code, src/llm/llm_weight.adb:277-292) or -1;
+ * dims[0] is ne0 (in_dim of a weight), dims[1] ne1 (out_dim). */
+typedef struct aspida_gguf aspida_gguf;
+typedef struct aspida_gguf_tensor_info {
+  const char *name;       /* valid until aspida_gguf_close */
+  int ggml_type, kind, n_dims;
+  long long dims[4];
+  long long file_offset;  /* absolute byte offset of the data in the file */
+  long long bytes;
+} aspida_gguf_tensor_info;
+/* NULL on a malformed or unreadable file; aspida_gguf_error() says why. */
+aspida_gguf *aspida_gguf_open(const char *path);
+const char *aspida_gguf_error(void);
+void aspida_gguf_close(aspida_gguf *g);
+int aspida_gguf_version(const aspida_gguf *g);
+long long aspida_gguf_alignment(const aspida_gguf *g);
+long long aspida_gguf_data_start(const aspida_gguf *g);
+long long aspida_gguf_tensor_count(const aspida_gguf *g);
+long long aspida_gguf_meta_count(const aspida_gguf *g);
+/* A metadata value as text (arrays as "[array: N]"), or NULL. */
+const char *aspida_gguf_meta(const aspida_gguf *g, const char *key);
+/* Index of the tensor named `name`, or -1. */
+long long aspida_gguf_find(const aspida_gguf *g, const char *name);
+int aspida_gguf_tensor(const aspida_gguf *g, long long i, aspida_gguf_tensor_info *out);
+/* Copy tensor i's bytes to dst (cap >= its byte size); returns the byte count
+ * or a negative errno. */
+long long aspida_gguf_read(const aspida_gguf *g, long long i, void *dst, long long cap);
+
 /* Split override for the packed kernels (aspida_kq_packed_plan): waves per
  * workgroup (a power of two <= 16) and workgroups per tile, applied to every
  * shape whose in_dim / 256 they divide; 0, 0 restores the built-in choice.
