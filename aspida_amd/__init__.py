@@ -60,6 +60,7 @@ def load(path=None):
         "aspida_kq_packed_bytes": (ctypes.c_longlong, [I, I, I]),
         "aspida_kq_pack_dev": (I, [I, P, I, I, P, P]),
         "aspida_kq_packed_plan": (I, [I, I, P, P, P]),
+        "aspida_kq_matvec_plan": (I, [I, I, I, P, P, P]),
         "aspida_kq_unpack_dev": (I, [I, P, I, I, P, P]),
         "aspida_kq_matvec_packed_dev": (I, [I, P, I, I, P, P, P]),
         "aspida_kq_matmul_packed_dev": (I, [I, P, I, I, I, P, P, P]),
@@ -79,6 +80,7 @@ def load(path=None):
         "aspida_kq_chain_workgroups": (I, [P]),
         "aspida_kq_chain_destroy": (None, [P]),
         "aspida_kq_set_packed_plan": (I, [I, I]),
+        "aspida_kq_set_mv_engine": (I, [I]),
         "aspida_kq_set_mv_config": (I, [I, I]),
     }
     for name, (res, args) in sig.items():
@@ -187,6 +189,15 @@ class DeviceOps:
                  "aspida_kq_packed_plan")
         return tuple(a.value for a in v)
 
+    def matvec_plan(self, kind, in_dim, out_dim):
+        """(uses the MFMA kernel, waves per workgroup, workgroups per tile,
+        columns per wave) of aspida_kq_matvec_packed_dev for this kind."""
+        v = [ctypes.c_int(0) for _ in range(3)]
+        rc = self.lib.aspida_kq_matvec_plan(kind, in_dim, out_dim, *[ctypes.byref(a) for a in v])
+        if rc < 0:
+            raise RuntimeError(f"aspida_kq_matvec_plan failed with code {rc}")
+        return (rc == 1,) + tuple(a.value for a in v)
+
     def pack(self, kind, w, in_dim, out_dim, packed, stream=0):
         self._ok(self.lib.aspida_kq_pack_dev(kind, w, in_dim, out_dim, packed, stream), "aspida_kq_pack_dev")
 
@@ -255,6 +266,10 @@ class DeviceOps:
 
     def set_mv_config(self, rows_per_wave=0, waves_per_cu=16):
         self._ok(self.lib.aspida_kq_set_mv_config(rows_per_wave, waves_per_cu), "aspida_kq_set_mv_config")
+
+    def set_mv_engine(self, engine):
+        """0: MFMA for Q4_K (default), 1: the VALU kernel for every kind."""
+        self._ok(self.lib.aspida_kq_set_mv_engine(engine), "aspida_kq_set_mv_engine")
 
 
 class KqStep(ctypes.Structure):

@@ -534,6 +534,19 @@ extern "C" int aspida_kq_packed_plan(int in_dim, int out_dim, int* waves_per_gro
   return 0;
 }
 
+extern "C" int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int* waves_per_group, int* groups_per_tile,
+                                     int* columns_per_wave) {
+  if (!valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || !waves_per_group || !groups_per_tile ||
+      !columns_per_wave)
+    return -EINVAL;
+  const bool mfma = kq::matvec_mfma_takes(kind);
+  const kq::PackedPlan p = mfma ? kq::mfma_plan(in_dim, out_dim) : kq::packed_plan(in_dim, out_dim);
+  *waves_per_group = p.nw;
+  *groups_per_tile = p.ks;
+  *columns_per_wave = p.spw;
+  return mfma ? 1 : 0;
+}
+
 extern "C" int aspida_kq_pack_dev(int kind, const void* w, int in_dim, int out_dim, void* packed, void* stream) {
   if (!w || !packed || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0) return -EINVAL;
   return check(kq::launch_pack(kind, w, in_dim, out_dim, packed, false, (hipStream_t)stream), "aspida_kq_pack_dev");
@@ -779,6 +792,12 @@ extern "C" void aspida_kq_chain_destroy(void* chain) { kq::chain_destroy((kq::Ch
 extern "C" int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile) {
   if (waves_per_group < 0 || groups_per_tile < 0) return -EINVAL;
   kq::set_packed_plan_override(waves_per_group, groups_per_tile);
+  return 0;
+}
+
+extern "C" int aspida_kq_set_mv_engine(int engine) {
+  if (engine < 0 || engine > 1) return -EINVAL;
+  kq::set_matvec_engine(engine);
   return 0;
 }
 

@@ -44,6 +44,8 @@ struct PackedPlan {
   int nw, ks, spw;
 };
 PackedPlan packed_plan(int in_dim, int out_dim);
+// The split of the MFMA matvec (kq_mv_mfma.hip); nw <= 8.
+PackedPlan mfma_plan(int in_dim, int out_dim);
 // Process-wide override of packed_plan for tuning (nw a power of two <= 16,
 // nw * ks dividing in_dim / 256; anything else, or 0, restores the choice).
 void set_packed_plan_override(int nw, int ks);
@@ -85,6 +87,15 @@ hipError_t launch_matmul_packed_valu(int kind, const void* P, int in_dim, int ou
                                      float* part, unsigned* count, hipStream_t s);
 
 hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void* dst, bool unpack, hipStream_t s);
+
+// Batch-1 packed matvec on MFMA (kq_mv_mfma.hip), same arguments, workspace
+// and counters as launch_matvec_packed, which routes here for the kinds it
+// takes.  set_matvec_engine(1) keeps every kind on the VALU kernel
+// (comparison), 0 restores the default.
+void set_matvec_engine(int engine);
+bool matvec_mfma_takes(int kind);
+hipError_t launch_matvec_mfma(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y, float* part,
+                              unsigned* count, hipStream_t s);
 
 // y = W x for packed W; x is 16-byte aligned.  Launches that share a
 // workspace must be ordered (one stream).

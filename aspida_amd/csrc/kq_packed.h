@@ -239,6 +239,70 @@ __device__ __forceinline__ float2 staged_dot2(const typename Packed<KIND>::R& rg
   }
   return make_float2(g, u);
 }
+// Sum of the NW waves' partial dots (LDS) and of the tile's ks = gridDim.y
+// workgroups (workspace), then y.  `gtile` indexes the workspace and
+// counters (tiles of every segment of a launch), `tile` the rows of y.
+//
+// Cross-workgroup sum: the partials and the counter are device-scope (sc1)
+// atomics, which bypass the per-XCD L2s, so no agent-scope fence -- an L2
+// write-back and invalidate on this chip -- is needed: the wait below retires
+// the partial store before the arrival is counted, and the last arrival reads
+// the partials only after its counter update returned, adding them in
+// ascending order.
+template <int NW>
+__device__ __forceinline__ void mv_epilogue(float acc, int gtile, int tile, int out_rows, float* __restrict__ y,
+                                            float* __restrict__ part, unsigned* __restrict__ count) {
+  __shared__ float red[NW > 1 ? NW * 64 : 1];
+  __shared__ unsigned is_last;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = gridDim.y;
+  if (NW > 1) {
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+      float t = red[lane];
+#pragma unroll
+      for (int k = 1; k < NW; ++k) t += red[k * 64 + lane];
+      acc = t;
+    }
+  }
+  const int row = tile * 64 + lane;
+  if (ks == 1) {
+    if (w == 0 && row < out_rows) y[row] = acc;
+    return;
+  }
+  const size_t ntiles = gridDim.x;
+  if (w == 0)
+    __hip_atomic_store(&part[((size_t)blockIdx.y * ntiles + gtile) * 64 + lane], acc, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(&count[(size_t)gtile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks - 1)
+                  ? 1u
+                  : 0u;
+  __syncthreads();
+  if (is_last && w == 0) {
+    // Eight partials in flight at a time, added in ascending k.
+    float t = 0.f;
+    for (int k0 = 0; k0 < ks; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = k0 + u < ks ? __hip_atomic_load(&part[((size_t)(k0 + u) * ntiles + gtile) * 64 + lane],
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                           : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < ks) t += v[u];
+    }
+    if (row < out_rows) y[row] = t;
+    if (lane == 0)
+      __hip_atomic_store(&count[(size_t)gtile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 #endif  // KQ_HOST_EMULATION
 
 }  // namespace kq

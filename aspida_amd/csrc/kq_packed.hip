@@ -52,71 +52,6 @@ __device__ __forceinline__ float columns_dot(const uint8_t* __restrict__ g, cons
   return acc + sb_dot<KIND>(r, xs + (size_t)(spw - 1) * 256, lane);
 }
 
-// Sum of the NW waves' partial dots (LDS) and of the tile's ks = gridDim.y
-// workgroups (workspace), then y.  `gtile` indexes the workspace and
-// counters (tiles of every segment of a launch), `tile` the rows of y.
-//
-// Cross-workgroup sum: the partials and the counter are device-scope (sc1)
-// atomics, which bypass the per-XCD L2s, so no agent-scope fence -- an L2
-// write-back and invalidate on this chip -- is needed: the wait below retires
-// the partial store before the arrival is counted, and the last arrival reads
-// the partials only after its counter update returned, adding them in
-// ascending order.
-template <int NW>
-__device__ __forceinline__ void mv_epilogue(float acc, int gtile, int tile, int out_rows, float* __restrict__ y,
-                                            float* __restrict__ part, unsigned* __restrict__ count) {
-  __shared__ float red[NW > 1 ? NW * 64 : 1];
-  __shared__ unsigned is_last;
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ks = gridDim.y;
-  if (NW > 1) {
-    red[w * 64 + lane] = acc;
-    __syncthreads();
-    if (w == 0) {
-      float t = red[lane];
-#pragma unroll
-      for (int k = 1; k < NW; ++k) t += red[k * 64 + lane];
-      acc = t;
-    }
-  }
-  const int row = tile * 64 + lane;
-  if (ks == 1) {
-    if (w == 0 && row < out_rows) y[row] = acc;
-    return;
-  }
-  const size_t ntiles = gridDim.x;
-  if (w == 0)
-    __hip_atomic_store(&part[((size_t)blockIdx.y * ntiles + gtile) * 64 + lane], acc, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0)
-    is_last = __hip_atomic_fetch_add(&count[(size_t)gtile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks - 1)
-                  ? 1u
-                  : 0u;
-  __syncthreads();
-  if (is_last && w == 0) {
-    // Eight partials in flight at a time, added in ascending k.
-    float t = 0.f;
-    for (int k0 = 0; k0 < ks; k0 += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        v[u] = k0 + u < ks ? __hip_atomic_load(&part[((size_t)(k0 + u) * ntiles + gtile) * 64 + lane],
-                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                           : 0.f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (k0 + u < ks) t += v[u];
-    }
-    if (row < out_rows) y[row] = t;
-    if (lane == 0)
-      __hip_atomic_store(&count[(size_t)gtile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
 template <int KIND, int NW, bool PF>
 __global__ __launch_bounds__(64 * NW) void kq_mv_packed(const uint8_t* __restrict__ P, int nsb, int out_rows,
                                                        const float* __restrict__ x, float* __restrict__ y, int spw,
@@ -264,9 +199,46 @@ PackedPlan packed_plan(int in_dim, int out_dim) {
   return p;
 }
 
+// Split of the MFMA matvec (kq_mv_mfma.hip).  One column per wave (no
+// prefetch: ~110 registers, 16 waves per CU) in workgroups of up to 4 waves,
+// fewer when that would leave less than a workgroup per CU; only matrices of
+// more than 32 columns per CU take several columns per wave (with prefetch,
+// ~190 registers), enough for one round of 8 waves per CU.  Measured on
+// MI355X at the Llama-3-8B shapes, one column per wave in 4-wave groups was
+// the fastest split (28672x4096, 4096x4096).
+PackedPlan mfma_plan(int in_dim, int out_dim) {
+  static const int cus = device_cus();
+  const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
+  PackedPlan p{1, 1, nsb};
+  {
+    const int onw = g_plan_nw, oks = g_plan_ks;
+    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && onw <= 8 && nsb % (onw * oks) == 0) {
+      p.nw = onw;
+      p.ks = oks;
+      p.spw = nsb / (onw * oks);
+      return p;
+    }
+  }
+  p.spw = 1;
+  if ((long)ntiles * nsb > 32L * cus) {
+    const long target = 8L * cus;
+    for (int spw = 1; spw <= nsb; ++spw) {
+      if (nsb % spw) continue;
+      p.spw = spw;
+      if ((long)ntiles * (nsb / spw) <= target) break;
+    }
+  }
+  const int cols = nsb / p.spw;
+  int nw = 1;
+  while (nw * 2 <= 4 && cols % (nw * 2) == 0 && (long)ntiles * (cols / (nw * 2)) >= cus) nw *= 2;
+  p.nw = nw;
+  p.ks = cols / nw;
+  return p;
+}
+
 size_t packed_workspace_floats(int in_dim, int out_dim) {
-  const PackedPlan p = packed_plan(in_dim, out_dim);
-  return p.ks > 1 ? (size_t)p.ks * ((out_dim + 63) / 64) * 64 : 0;
+  const int ks = std::max(packed_plan(in_dim, out_dim).ks, mfma_plan(in_dim, out_dim).ks);
+  return ks > 1 ? (size_t)ks * ((out_dim + 63) / 64) * 64 : 0;
 }
 
 size_t packed_counters(int out_dim) { return (size_t)(out_dim + 63) / 64 * COUNTER_STRIDE; }
@@ -296,6 +268,7 @@ static hipError_t launch_mvp_kind(const uint8_t* P, int in_dim, int out_dim, con
 
 hipError_t launch_matvec_packed(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y,
                                 float* part, unsigned* count, hipStream_t s) {
+  if (matvec_mfma_takes(kind)) return launch_matvec_mfma(kind, P, in_dim, out_dim, x, y, part, count, s);
   const uint8_t* w = (const uint8_t*)P;
   switch (kind) {
     case Q4_K: return launch_mvp_kind<Q4_K>(w, in_dim, out_dim, x, y, part, count, s);

@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--only", choices=["small", "moe", "kquant"],
                     help="run just this table (no decode line): for profiling one workload")
+    ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
+                    help="batch-1 engine: 0 = MFMA for Q4_K (default), 1 = the VALU kernel for every kind")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
@@ -70,9 +72,11 @@ class Decoder:
     """Device-resident Llama-3-8B Q4_K_M weights, in the packed layout of the
     batch-1 kernels, and the per-token launch list."""
 
-    def __init__(self, torch, aa, synth, seed):
+    def __init__(self, torch, aa, synth, seed, engine=0):
         self.torch, self.dev = torch, aa.DeviceOps()
         self.aa = aa
+        self.engine = engine
+        self.dev.set_mv_engine(engine)
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
 
@@ -146,11 +150,17 @@ class Decoder:
 
 
 def kernel_name(dec, op):
-    """The kernel symbol a launch runs: kq_mv_packed<kind, waves, prefetch> or
+    """The kernel symbol a launch runs: kq_mv_mfma_q4k<waves, prefetch> (Q4_K
+    on the matrix cores), kq_mv_packed<kind, waves, prefetch> or
     kq_mv_packed2<kind_a, kind_b, waves, prefetch> (the launch split is the
-    library's, aspida_kq_packed_plan)."""
+    library's: aspida_kq_matvec_plan, aspida_kq_packed_plan)."""
     rows = sum(-(-o // 64) * 64 for _, _, _, o, _, _ in op)
-    nw, _, spw = dec.dev.packed_plan(op[0][2], rows)
+    if len(op) == 1:
+        mfma, nw, _, spw = dec.dev.matvec_plan(op[0][0], op[0][2], rows)
+        if mfma:
+            return f"kq_mv_mfma_q4k<{nw}, {'true' if spw > 1 else 'false'}>"
+    else:
+        nw, _, spw = dec.dev.packed_plan(op[0][2], rows)
     pf = "true" if spw > 1 else "false"
     kinds = ", ".join(str(m[0]) for m in op)
     return f"kq_mv_packed{'2' if len(op) > 1 else ''}<{kinds}, {nw}, {pf}>"
@@ -462,7 +472,7 @@ def main():
         fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
         return
-    dec = Decoder(torch, aa, synth, args.seed)
+    dec = Decoder(torch, aa, synth, args.seed, args.mv_engine)
     torch.cuda.synchronize()
 
     def timed(step_fn, steps, warmup):

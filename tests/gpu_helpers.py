@@ -9,6 +9,11 @@ import oracle
 # sum_i |w_i x_i| of that output.  Both sides accumulate in f32 in different
 # orders; the bar the hot path must meet is 1e-3.
 MV_RTOL = 2e-5
+# The batch-1 MFMA kernel against the oracle: the matrix cores' sums lose bits
+# when one product dwarfs the others (measured ~3e-5 of sum |w x| with 1e4x
+# outliers in a column), so activations with such outliers get this bound;
+# still 10x inside the 1e-3 bar.
+MFMA_RTOL = 1e-4
 
 
 def torch_cuda():

@@ -15,7 +15,8 @@ import pytest
 import aspida_amd as aa
 import oracle
 from aspida_amd import synth
-from gpu_helpers import abs_dot_scale, assert_close_scaled, ncpu, stream, sync, to_dev, torch_cuda
+from gpu_helpers import (MFMA_RTOL, MV_RTOL, abs_dot_scale, assert_close_scaled, ncpu, stream, sync, to_dev,
+                         torch_cuda)
 
 pytestmark = pytest.mark.gpu
 
@@ -327,3 +328,52 @@ def test_errors_leave_nan_and_code(gpu):
     y = gpu.matvec(np.zeros(144, np.uint8), 0, 256, 4, np.ones(256, np.float32))
     assert np.all(np.isnan(y)) and gpu.last_error() != 0
     assert gpu.last_error() == 0
+
+
+def _x_variants(in_dim, gen):
+    """Activations that stress the MFMA kernel's per-column scaling: plain,
+    outliers (x 1e4), tiny (1e-28), huge (1e30), one all-zero column, and mixed
+    magnitudes inside a column."""
+    base = synth.activations_np(in_dim, gen)
+    out = {"plain": base}
+    o = base.copy()
+    o[gen.integers(0, in_dim, 7)] *= 1e4
+    out["outliers"] = o
+    out["tiny"] = (base * 1e-28).astype(np.float32)
+    out["huge"] = (base * 1e30).astype(np.float32)
+    z = base.copy()
+    z[256:512] = 0.0
+    out["zero_column"] = z
+    m = base.copy()
+    m[::3] *= 1e-6
+    m[1::5] *= 1e3
+    out["mixed"] = m
+    return out
+
+
+@pytest.mark.parametrize("engine", [0, 1], ids=["mfma", "valu"])
+def test_q4k_engines_activation_range(engine, dev):
+    """Both batch-1 engines for Q4_K against the oracle, over activations whose
+    magnitudes span the f32 range."""
+    torch = torch_cuda()
+    gen = synth.rng(4040 + engine)
+    dev.set_mv_engine(engine)
+    try:
+        for out_dim, in_dim in [(130, 4096), (4096, 1024), (300, 14336), (28672, 512)]:
+            w = synth.weight_np(aa.Q4_K, out_dim, in_dim, gen)
+            dp = torch.empty(dev.packed_bytes(aa.Q4_K, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+            dw = to_dev(w)
+            dev.pack(aa.Q4_K, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+            for name, x in _x_variants(in_dim, gen).items():
+                print(f"engine {engine} Q4_K {out_dim}x{in_dim} x={name}", flush=True)
+                dx = to_dev(x)
+                dy = torch.full((out_dim,), float("nan"), dtype=torch.float32, device="cuda")
+                dev.matvec_packed(aa.Q4_K, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
+                sync()
+                want = oracle.qmatvec(aa.Q4_K, w, in_dim, out_dim, x, nthreads=ncpu())
+                rtol = MFMA_RTOL if engine == 0 and name in ("outliers", "mixed") else MV_RTOL
+                r = assert_close_scaled(dy.cpu().numpy(), want, abs_dot_scale(aa.Q4_K, w, in_dim, out_dim, x),
+                                        rtol=rtol, what=f"engine {engine} {out_dim}x{in_dim} {name}")
+                print(f"  max err / sum|wx| = {r:.2e}", flush=True)
+    finally:
+        dev.set_mv_engine(0)
