@@ -268,7 +268,7 @@ class DeviceOps:
         self._ok(self.lib.aspida_kq_set_mv_config(rows_per_wave, waves_per_cu), "aspida_kq_set_mv_config")
 
     def set_mv_engine(self, engine):
-        """0: MFMA for Q4_K (default), 1: the VALU kernel for every kind."""
+        """0: MFMA for Q4_K and Q6_K (default), 1: the VALU kernel for every kind."""
         self._ok(self.lib.aspida_kq_set_mv_engine(engine), "aspida_kq_set_mv_engine")
 
 

@@ -540,7 +540,7 @@ extern "C" int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int* wav
       !columns_per_wave)
     return -EINVAL;
   const bool mfma = kq::matvec_mfma_takes(kind);
-  const kq::PackedPlan p = mfma ? kq::mfma_plan(in_dim, out_dim) : kq::packed_plan(in_dim, out_dim);
+  const kq::PackedPlan p = mfma ? kq::mfma_plan(kind, in_dim, out_dim) : kq::packed_plan(in_dim, out_dim);
   *waves_per_group = p.nw;
   *groups_per_tile = p.ks;
   *columns_per_wave = p.spw;

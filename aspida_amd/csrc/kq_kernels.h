@@ -44,8 +44,8 @@ struct PackedPlan {
   int nw, ks, spw;
 };
 PackedPlan packed_plan(int in_dim, int out_dim);
-// The split of the MFMA matvec (kq_mv_mfma.hip); nw <= 8.
-PackedPlan mfma_plan(int in_dim, int out_dim);
+// The split of the MFMA matvec (kq_mv_mfma.hip) for a kind.
+PackedPlan mfma_plan(int kind, int in_dim, int out_dim);
 // Process-wide override of packed_plan for tuning (nw a power of two <= 16,
 // nw * ks dividing in_dim / 256; anything else, or 0, restores the choice).
 void set_packed_plan_override(int nw, int ks);
@@ -96,6 +96,11 @@ void set_matvec_engine(int engine);
 bool matvec_mfma_takes(int kind);
 hipError_t launch_matvec_mfma(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y, float* part,
                               unsigned* count, hipStream_t s);
+// The fused pair on MFMA when both kinds are MFMA kinds (launch_matvec2_packed
+// routes here).
+bool matvec2_mfma_takes(int kind_a, int kind_b);
+hipError_t launch_matvec2_mfma(int kind_a, const void* Pa, int out_a, float* ya, int kind_b, const void* Pb, int out_b,
+                               float* yb, int in_dim, const float* x, float* part, unsigned* count, hipStream_t s);
 
 // y = W x for packed W; x is 16-byte aligned.  Launches that share a
 // workspace must be ordered (one stream).

@@ -199,45 +199,56 @@ PackedPlan packed_plan(int in_dim, int out_dim) {
   return p;
 }
 
-// Split of the MFMA matvec (kq_mv_mfma.hip).  One column per wave (no
-// prefetch: ~110 registers, 16 waves per CU) in workgroups of up to 4 waves,
-// fewer when that would leave less than a workgroup per CU; only matrices of
-// more than 32 columns per CU take several columns per wave (with prefetch,
-// ~190 registers), enough for one round of 8 waves per CU.  Measured on
-// MI355X at the Llama-3-8B shapes, one column per wave in 4-wave groups was
-// the fastest split (28672x4096, 4096x4096).
-PackedPlan mfma_plan(int in_dim, int out_dim) {
+// Split of the MFMA matvec (kq_mv_mfma.hip), fitted to measurements on
+// MI355X at the Llama-3-8B Q4_K_M shapes (launch time per split, cold HBM):
+//   * a tile per CU or more, 16 columns: whole tiles by 16 one-column waves (no
+//     cross-workgroup sum, whose atomic round trip holds every workgroup ~1 us
+//     longer; 28672x4096: 15.3 us against 16.4 for 4 workgroups per tile),
+//     or 8-wave halves once the tiles are 4 per CU (128256x4096: 80 us
+//     against 82);
+//   * a tile per CU or more, other widths: whole tiles by up to 8 waves (4 for
+//     Q6_K, whose prefetching waves hold ~260 registers) of several columns;
+//   * narrower matrices: one column per wave, the most waves per workgroup
+//     (<= 8) that still leave >= 150 workgroups, at least 2 (4096x14336 Q6_K
+//     8 x 7 groups: 12.5 us against 14.5 for 4 x 14; 4096x4096: 4 x 4;
+//     1024x4096: 2 x 8).
+PackedPlan mfma_plan(int kind, int in_dim, int out_dim) {
   static const int cus = device_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   PackedPlan p{1, 1, nsb};
   {
     const int onw = g_plan_nw, oks = g_plan_ks;
-    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && onw <= 8 && nsb % (onw * oks) == 0) {
+    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && nsb % (onw * oks) == 0 &&
+        (onw <= 8 || (onw == 16 && nsb == onw * oks))) {
       p.nw = onw;
       p.ks = oks;
       p.spw = nsb / (onw * oks);
       return p;
     }
   }
-  p.spw = 1;
-  if ((long)ntiles * nsb > 32L * cus) {
-    const long target = 8L * cus;
-    for (int spw = 1; spw <= nsb; ++spw) {
-      if (nsb % spw) continue;
-      p.spw = spw;
-      if ((long)ntiles * (nsb / spw) <= target) break;
+  if (ntiles >= cus) {
+    if (nsb == 16) {
+      p.spw = 1;
+      p.nw = ntiles >= 4 * cus ? 8 : 16;
+      p.ks = nsb / p.nw;
+      return p;
     }
+    p.ks = 1;
+    p.nw = pow2_divisor_upto(nsb, kind == Q6_K ? 4 : 8);
+    p.spw = nsb / p.nw;
+    return p;
   }
-  const int cols = nsb / p.spw;
-  int nw = 1;
-  while (nw * 2 <= 4 && cols % (nw * 2) == 0 && (long)ntiles * (cols / (nw * 2)) >= cus) nw *= 2;
+  p.spw = 1;
+  int nw = pow2_divisor_upto(nsb, 8);
+  while (nw > 2 && (long)ntiles * (nsb / nw) < 150) nw /= 2;
   p.nw = nw;
-  p.ks = cols / nw;
+  p.ks = nsb / nw;
   return p;
 }
 
 size_t packed_workspace_floats(int in_dim, int out_dim) {
-  const int ks = std::max(packed_plan(in_dim, out_dim).ks, mfma_plan(in_dim, out_dim).ks);
+  const int ks = std::max({packed_plan(in_dim, out_dim).ks, mfma_plan(Q4_K, in_dim, out_dim).ks,
+                           mfma_plan(Q6_K, in_dim, out_dim).ks});
   return ks > 1 ? (size_t)ks * ((out_dim + 63) / 64) * 64 : 0;
 }
 
@@ -321,6 +332,8 @@ static hipError_t launch_mv2_pair(const void* Pa, int out_a, float* ya, const vo
 hipError_t launch_matvec2_packed(int kind_a, const void* Pa, int out_a, float* ya, int kind_b, const void* Pb,
                                  int out_b, float* yb, int in_dim, const float* x, float* part, unsigned* count,
                                  hipStream_t s) {
+  if (matvec2_mfma_takes(kind_a, kind_b))
+    return launch_matvec2_mfma(kind_a, Pa, out_a, ya, kind_b, Pb, out_b, yb, in_dim, x, part, count, s);
 #define KQ_PAIR_GO(A, B) \
   if (kind_a == A && kind_b == B) return launch_mv2_pair<A, B>(Pa, out_a, ya, Pb, out_b, yb, in_dim, x, part, count, s);
   KQ_PAIRS(KQ_PAIR_GO)

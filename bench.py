@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--only", choices=["small", "moe", "kquant"],
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
-                    help="batch-1 engine: 0 = MFMA for Q4_K (default), 1 = the VALU kernel for every kind")
+                    help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
@@ -150,16 +150,24 @@ class Decoder:
 
 
 def kernel_name(dec, op):
-    """The kernel symbol a launch runs: kq_mv_mfma_q4k<waves, prefetch> (Q4_K
-    on the matrix cores), kq_mv_packed<kind, waves, prefetch> or
+    """The kernel symbol a launch runs: kq_mv_mfma<kind, waves, prefetch> and
+    kq_mv_mfma2<kind_a, kind_b, waves, prefetch> (Q4_K and Q6_K on the matrix
+    cores), kq_mv_packed<kind, waves, prefetch> or
     kq_mv_packed2<kind_a, kind_b, waves, prefetch> (the launch split is the
     library's: aspida_kq_matvec_plan, aspida_kq_packed_plan)."""
     rows = sum(-(-o // 64) * 64 for _, _, _, o, _, _ in op)
+    kinds = [m[0] for m in op]
     if len(op) == 1:
-        mfma, nw, _, spw = dec.dev.matvec_plan(op[0][0], op[0][2], rows)
+        mfma, nw, _, spw = dec.dev.matvec_plan(kinds[0], op[0][2], rows)
         if mfma:
-            return f"kq_mv_mfma_q4k<{nw}, {'true' if spw > 1 else 'false'}>"
+            return f"kq_mv_mfma<{kinds[0]}, {nw}, {'true' if spw > 1 else 'false'}>"
     else:
+        aa = dec.aa
+        # the pair runs on MFMA when both kinds do, with the wider kind's split
+        mf = [dec.dev.matvec_plan(k, op[0][2], rows) for k in kinds]
+        if all(m[0] for m in mf):
+            _, nw, _, spw = dec.dev.matvec_plan(aa.Q6_K if aa.Q6_K in kinds else kinds[0], op[0][2], rows)
+            return f"kq_mv_mfma2<{kinds[0]}, {kinds[1]}, {nw}, {'true' if spw > 1 else 'false'}>"
         nw, _, spw = dec.dev.packed_plan(op[0][2], rows)
     pf = "true" if spw > 1 else "false"
     kinds = ", ".join(str(m[0]) for m in op)

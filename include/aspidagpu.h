@@ -106,7 +106,7 @@ int aspida_kq_unpack_dev(int kind, const void *packed, int in_dim, int out_dim, 
  * tile and super-block columns per wave (their product is in_dim / 256). */
 /* The kernel and split aspida_kq_matvec_packed_dev uses for a kind and shape
  * under the current engine (aspida_kq_set_mv_engine): returns 1 for the
- * matrix-core kernel kq_mv_mfma_q4k<waves, prefetch>, 0 for the vector kernel
+ * matrix-core kernel kq_mv_mfma<kind, waves, prefetch>, 0 for the vector kernel
  * kq_mv_packed<kind, waves, prefetch>, or -EINVAL.  No reference counterpart. */
 int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int *waves_per_group, int *groups_per_tile,
                           int *columns_per_wave);
@@ -279,8 +279,9 @@ long long aspida_gguf_read(const aspida_gguf *g, long long i, void *dst, long lo
 int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile);
 
 /* Engine of the batch-1 packed matvec (aspida_kq_matvec_packed_dev and the
- * calls built on it): 0 = matrix cores (MFMA) for Q4_K, the vector kernel for
- * the other kinds (the default); 1 = the vector kernel for every kind.
+ * calls built on it): 0 = matrix cores (MFMA) for Q4_K and Q6_K, the vector
+ * kernel for the other kinds (the default); 1 = the vector kernel for every
+ * kind.
  * Process-wide; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mv_engine(int engine);

@@ -70,19 +70,25 @@ def _packed_matmul(kind, w, X, in_dim, out_dim):
 
 
 def _packed_rows(kind, w, X, in_dim, out_dim):
-    """The batch-1 packed matvec of every row of X (same packed image)."""
+    """The batch-1 packed matvec of every row of X (same packed image) on the
+    VALU kernel, whose sums the multi-vector kernel reproduces bit for bit
+    (Q4_K and Q6_K run batch 1 on MFMA by default)."""
     torch = torch_cuda()
     dev = aa.DeviceOps()
     dw = to_dev(w)
     dp = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
     dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
     out = []
-    for b in range(X.shape[0]):
-        dx = to_dev(np.ascontiguousarray(X[b], np.float32))
-        dy = torch.full((out_dim,), float("nan"), device="cuda")
-        dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
-        sync()
-        out.append(dy.cpu().numpy())
+    dev.set_mv_engine(1)
+    try:
+        for b in range(X.shape[0]):
+            dx = to_dev(np.ascontiguousarray(X[b], np.float32))
+            dy = torch.full((out_dim,), float("nan"), device="cuda")
+            dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
+            sync()
+            out.append(dy.cpu().numpy())
+    finally:
+        dev.set_mv_engine(0)
     return np.stack(out)
 
 

@@ -352,27 +352,32 @@ def _x_variants(in_dim, gen):
 
 
 @pytest.mark.parametrize("engine", [0, 1], ids=["mfma", "valu"])
-def test_q4k_engines_activation_range(engine, dev):
-    """Both batch-1 engines for Q4_K against the oracle, over activations whose
-    magnitudes span the f32 range."""
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+def test_engines_activation_range(kind, engine, dev):
+    """Both batch-1 engines for Q4_K and Q6_K against the oracle, over
+    activations whose magnitudes span the f32 range, at shapes that take every
+    split of the MFMA kernel (16-wave whole tiles, 4-wave groups over several
+    workgroups, prefetching waves of several columns)."""
     torch = torch_cuda()
-    gen = synth.rng(4040 + engine)
+    gen = synth.rng(4040 + engine + 10 * kind)
     dev.set_mv_engine(engine)
     try:
-        for out_dim, in_dim in [(130, 4096), (4096, 1024), (300, 14336), (28672, 512)]:
-            w = synth.weight_np(aa.Q4_K, out_dim, in_dim, gen)
-            dp = torch.empty(dev.packed_bytes(aa.Q4_K, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+        for out_dim, in_dim in [(130, 4096), (4096, 1024), (300, 14336), (28672, 512), (16448, 4096),
+                                (16448, 2048)]:
+            w = synth.weight_np(kind, out_dim, in_dim, gen)
+            dp = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
             dw = to_dev(w)
-            dev.pack(aa.Q4_K, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+            dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+            plan = dev.matvec_plan(kind, in_dim, out_dim)
             for name, x in _x_variants(in_dim, gen).items():
-                print(f"engine {engine} Q4_K {out_dim}x{in_dim} x={name}", flush=True)
+                print(f"engine {engine} {aa.KIND_NAMES[kind]} {out_dim}x{in_dim} plan {plan} x={name}", flush=True)
                 dx = to_dev(x)
                 dy = torch.full((out_dim,), float("nan"), dtype=torch.float32, device="cuda")
-                dev.matvec_packed(aa.Q4_K, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
+                dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
                 sync()
-                want = oracle.qmatvec(aa.Q4_K, w, in_dim, out_dim, x, nthreads=ncpu())
+                want = oracle.qmatvec(kind, w, in_dim, out_dim, x, nthreads=ncpu())
                 rtol = MFMA_RTOL if engine == 0 and name in ("outliers", "mixed") else MV_RTOL
-                r = assert_close_scaled(dy.cpu().numpy(), want, abs_dot_scale(aa.Q4_K, w, in_dim, out_dim, x),
+                r = assert_close_scaled(dy.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x),
                                         rtol=rtol, what=f"engine {engine} {out_dim}x{in_dim} {name}")
                 print(f"  max err / sum|wx| = {r:.2e}", flush=True)
     finally:
