@@ -208,7 +208,7 @@ def kernel_events(torch, dec, stream, reps=5):
     return out
 
 
-TRAFFIC_FILE = os.path.join(HERE, "profiles", "kq_mv_packed_llama8b_decode_traffic.json")
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "kq_mv_mfma_llama8b_decode_traffic.json")
 
 
 def measured_traffic(kernel):
