@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <unordered_map>
@@ -174,7 +175,9 @@ struct MvWorkspace {
   int ensure(int in_dim, int out_dim, int batch = 1) {
     const size_t pf = batch > 1 ? kq::multi_workspace_floats(in_dim, out_dim) : kq::packed_workspace_floats(in_dim, out_dim);
     if (part.ensure(std::max<size_t>(pf, 64), "hipMalloc partials")) return -1;
-    if (batch > 1 && mm.ensure(kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, 64)), "hipMalloc mfma"))
+    if (batch > 1 && mm.ensure(std::max(kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, 64)),
+                                        kq::mm16_workspace_bytes(in_dim, out_dim)),
+                               "hipMalloc mfma"))
       return -1;
     const size_t want = kq::packed_counters(out_dim);
     if (want <= count.n) return 0;
@@ -183,21 +186,37 @@ struct MvWorkspace {
   }
 };
 
-// Y[batch][out] = X W^T over packed W on `st`: small batches on the
-// multi-vector VALU kernel (up to 4 vectors for the kinds with MFMA kernels,
-// where MFMA is faster from 5 on; 8 per launch for the others), larger Q4_K /
-// Q6_K batches on MFMA (64 activation rows per launch).
+// Y[batch][out] = X W^T over packed W on `st`.  Batch 1 is the matvec.
+// Otherwise, by g_mm_engine: 0 picks, 1 forces the multi-vector VALU kernel,
+// 2 the 64-vector and 3 the 16-vector MFMA kernel where the kind has one.
+// The pick (measured on MI355X, Q4_K): up to 4 vectors on VALU; 5-16 on the
+// 16-vector kernel; beyond 16 the 16-vector kernel in launches of 16 when
+// the matrix has at least MM16_MIN_UNITS (64-row tile, super-block column)
+// pairs to spread, else the 64-vector kernel, which then takes the batch in
+// fewer launches.  Q6_K: VALU up to 4, then the 64-vector kernel.
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
+constexpr long MM16_MIN_UNITS = 2048;
+std::atomic<int> g_mm_engine{0};
 hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
                          MvWorkspace& ws, hipStream_t st) {
   if (batch == 1)
     return kq::launch_matvec_packed(kind, P, in_dim, out_dim, X, Y, ws.part.p, ws.count.p, st);
-  if (batch > MULTI_MAX_BATCH_MFMA_KINDS && kq::mfma_kind(kind)) {
-    for (int b0 = 0; b0 < batch; b0 += 64) {
-      const int nb = std::min(64, batch - b0);
-      const hipError_t e = kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, X + (size_t)b0 * in_dim,
-                                                         Y + (size_t)b0 * out_dim, ws.mm.p, ws.count.p, st);
+  const int eng = g_mm_engine.load(std::memory_order_relaxed);
+  const long units = (long)((out_dim + 63) / 64) * (in_dim / 256);
+  const bool mm16 = kq::mm16_kind(kind) &&
+                    (eng == 3 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS &&
+                                  (batch <= 16 || units >= MM16_MIN_UNITS)));
+  const bool mm64 = !mm16 && kq::mfma_kind(kind) && (eng == 2 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS));
+  if (mm16 || mm64) {
+    const int step = mm16 ? 16 : 64;
+    for (int b0 = 0; b0 < batch; b0 += step) {
+      const int nb = std::min(step, batch - b0);
+      const float* xb = X + (size_t)b0 * in_dim;
+      float* yb = Y + (size_t)b0 * out_dim;
+      const hipError_t e = mm16 ? kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st)
+                                : kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p,
+                                                                ws.count.p, st);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -544,7 +563,7 @@ extern "C" int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int* wav
   *waves_per_group = p.nw;
   *groups_per_tile = p.ks;
   *columns_per_wave = p.spw;
-  return mfma ? 1 : 0;
+  return mfma ? (p.seq && p.spw > 1 ? 2 : 1) : 0;
 }
 
 extern "C" int aspida_kq_pack_dev(int kind, const void* w, int in_dim, int out_dim, void* packed, void* stream) {
@@ -795,9 +814,21 @@ extern "C" int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_til
   return 0;
 }
 
+extern "C" int aspida_kq_set_mfma_pipeline(int mode) {
+  if (mode < 0 || mode > 2) return -EINVAL;
+  kq::set_mfma_pipeline(mode);
+  return 0;
+}
+
 extern "C" int aspida_kq_set_mv_engine(int engine) {
   if (engine < 0 || engine > 1) return -EINVAL;
   kq::set_matvec_engine(engine);
+  return 0;
+}
+
+extern "C" int aspida_kq_set_mm_engine(int engine) {
+  if (engine < 0 || engine > 3) return -EINVAL;
+  g_mm_engine.store(engine, std::memory_order_relaxed);
   return 0;
 }
 

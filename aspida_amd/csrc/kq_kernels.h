@@ -42,13 +42,20 @@ hipError_t launch_dequant(int kind, const void* W, int in_dim, int out_dim, floa
 // per workgroup, ks workgroups per 64-row tile (nw * ks * spw == in_dim / 256).
 struct PackedPlan {
   int nw, ks, spw;
+  bool seq = false;  // MFMA kernel: columns one after another (one register set) even when spw > 1
 };
 PackedPlan packed_plan(int in_dim, int out_dim);
 // The split of the MFMA matvec (kq_mv_mfma.hip) for a kind.
 PackedPlan mfma_plan(int kind, int in_dim, int out_dim);
+// Tuning: 0 = the plan's choice, 1 = prefetching waves, 2 = sequential columns
+// (for splits with more than one column per wave).
+void set_mfma_pipeline(int mode);
 // Process-wide override of packed_plan for tuning (nw a power of two <= 16,
 // nw * ks dividing in_dim / 256; anything else, or 0, restores the choice).
 void set_packed_plan_override(int nw, int ks);
+// The override's workgroups per tile (0: none); the small-batch MFMA product
+// takes it as its column split too.
+int packed_plan_override_ks();
 
 // Bytes of the packed image of a [out_dim][in_dim] matrix (rows rounded up to
 // a multiple of 64); 0 for an invalid kind or shape.
@@ -77,6 +84,14 @@ bool mfma_kind(int kind);
 size_t mfma_workspace_bytes(int in_dim, int out_dim, int batch);
 hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X,
                                      float* Y, void* work, unsigned* count, hipStream_t s);
+
+// Up to 16 activation rows per launch on MFMA, dense in rows and vectors
+// (kq_mm16.hip): kinds it takes, workspace bytes (activation images and
+// partials), and the launcher; `count` as above.
+bool mm16_kind(int kind);
+size_t mm16_workspace_bytes(int in_dim, int out_dim);
+hipError_t launch_matmul_mm16(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
+                              void* work, unsigned* count, hipStream_t s);
 
 // ggml layout -> packed (unpack = false) or back (unpack = true).
 // Y[b][out] = W X[b] for nb <= 8 vectors over packed W on VALU

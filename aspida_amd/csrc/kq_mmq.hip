@@ -285,11 +285,11 @@ struct Q4Regs {
   uint2 wc[4];
 };
 
-template <int MB>
+template <int MB, int NB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kq_mm_mfma_q4k(MmArgs a) {
   constexpr int GB = 64 * 144, BP = 16 * MB;
-  __shared__ __attribute__((aligned(16))) _Float16 xb[2][BP * XROW];
-  __shared__ __attribute__((aligned(16))) _Float16 sb[2][BP * SROW];
+  __shared__ __attribute__((aligned(16))) _Float16 xb[NB][BP * XROW];
+  __shared__ __attribute__((aligned(16))) _Float16 sb[NB][BP * SROW];
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = 16 * w + j;  // weight row within the tile
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   xtile_store<MB>(xb[0], sb[0], xv, xsv);
   __syncthreads();
   for (int c = 0; c < a.spw; ++c) {
-    const int buf = c & 1;
+    const int buf = NB == 2 ? (c & 1) : 0;  // one buffer: a single column (host-checked)
     const bool more = c + 1 < a.spw;
     if (more) {
       load_w(s0 + c + 1, nxt);
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       acc[mb] -= (dmin * (1.f / XSUM_UNIT)) * D;
     }
     if (more) {
-      xtile_store<MB>(xb[buf ^ 1], sb[buf ^ 1], xv, xsv);
+      xtile_store<MB>(xb[(buf + 1) % NB], sb[(buf + 1) % NB], xv, xsv);
       cur = nxt;
     }
     __syncthreads();
@@ -372,11 +372,11 @@ struct Q6Regs {
   uint32_t wa[4], wb[4], wq[4];  // [hh * 2 + t]
 };
 
-template <int MB>
+template <int MB, int NB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kq_mm_mfma_q6k(MmArgs a) {
   constexpr int GB = 64 * 210, BP = 16 * MB;
-  __shared__ __attribute__((aligned(16))) _Float16 xb[2][BP * XROW];
-  __shared__ __attribute__((aligned(16))) _Float16 sb[2][BP * SROW];
+  __shared__ __attribute__((aligned(16))) _Float16 xb[NB][BP * XROW];
+  __shared__ __attribute__((aligned(16))) _Float16 sb[NB][BP * SROW];
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row = 16 * w + j;
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   xtile_store<MB>(xb[0], sb[0], xv, xsv);
   __syncthreads();
   for (int c = 0; c < a.spw; ++c) {
-    const int buf = c & 1;
+    const int buf = NB == 2 ? (c & 1) : 0;  // one buffer: a single column (host-checked)
     const bool more = c + 1 < a.spw;
     if (more) {
       load_w(s0 + c + 1, nxt);
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       acc[mb] -= (32.f * d * (1.f / XSUM_UNIT)) * D;
     }
     if (more) {
-      xtile_store<MB>(xb[buf ^ 1], sb[buf ^ 1], xv, xsv);
+      xtile_store<MB>(xb[(buf + 1) % NB], sb[(buf + 1) % NB], xv, xsv);
       cur = nxt;
     }
     __syncthreads();
@@ -477,6 +477,8 @@ bool mfma_kind(int kind) { return kind == Q4_K || kind == Q6_K; }
 static int mm_spw(int in_dim, int out_dim, int bp) {
   static const int cus = mm_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
+  const int oks = packed_plan_override_ks();
+  if (oks > 0 && nsb % oks == 0 && oks <= 256 / bp) return nsb / oks;
   const double target = 4.0 * cus;
   int best_spw = nsb;
   double best = 1e30;
@@ -527,11 +529,18 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
     hipLaunchKernelGGL(kq_xsplit<16>, dim3(bp), dim3(1024), 0, s, X, batch, in_dim, xh, xl, sh, sl, inv);
   const MmArgs a{(const uint8_t*)P, nsb, out_dim, batch, spw, xh, xl, sh, sl, inv, Y, part, count};
   const dim3 grid(ntiles, ks);
-#define KQ_MM(MB)                                                                            \
-  if (bp == 16 * MB) {                                                                       \
-    if (kind == Q4_K) hipLaunchKernelGGL(kq_mm_mfma_q4k<MB>, grid, dim3(256), 0, s, a);      \
-    else hipLaunchKernelGGL(kq_mm_mfma_q6k<MB>, grid, dim3(256), 0, s, a);                   \
-    return hipGetLastError();                                                                \
+  // One column per workgroup needs a single activation buffer: half the LDS,
+  // so more workgroups are resident at once.
+#define KQ_MM(MB)                                                                                  \
+  if (bp == 16 * MB) {                                                                             \
+    if (spw == 1) {                                                                                \
+      if (kind == Q4_K) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 1>), grid, dim3(256), 0, s, a);     \
+      else hipLaunchKernelGGL((kq_mm_mfma_q6k<MB, 1>), grid, dim3(256), 0, s, a);                  \
+    } else {                                                                                       \
+      if (kind == Q4_K) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 2>), grid, dim3(256), 0, s, a);     \
+      else hipLaunchKernelGGL((kq_mm_mfma_q6k<MB, 2>), grid, dim3(256), 0, s, a);                  \
+    }                                                                                              \
+    return hipGetLastError();                                                                      \
   }
   KQ_MM(1) KQ_MM(2) KQ_MM(4)
 #undef KQ_MM

@@ -318,7 +318,12 @@ struct MvShared {
 
 // Row `lane` of tile `tile`'s partial dot over super-block columns sb0 ..
 // sb0 + spw - 1 of packed matrix P (nsb columns), computed by this wave.
-template <int KIND, bool PF>
+// How a wave walks its columns: one column; two register sets in turn (the
+// next column's loads in flight during this one's work); one register set,
+// columns one after another (fewer registers, so more waves per CU).
+constexpr int MV_ONE = 0, MV_PF = 1, MV_SEQ = 2;
+
+template <int KIND, int PIPE>
 __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int nsb, int tile, int sb0, int spw,
                                               const float* __restrict__ x, uint4 (&img)[8][64], float* xsum,
                                               MvHdr<KIND>& hdr, int lane) {
@@ -335,8 +340,17 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
   float4 x0;
   c0.load(gp, lane);
   __builtin_memcpy(&x0, __builtin_assume_aligned(xp, 16), 16);
-  if (!PF) {  // one column per wave
+  if (PIPE == MV_ONE) {
     mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+  } else if (PIPE == MV_SEQ) {  // columns one after another: one register set, more waves per CU
+    for (int s = 0; s < spw; ++s) {
+      if (s > 0) {
+        asm volatile("" ::: "memory");  // the next column's loads stay after this column's work
+        c0.load(gp + (size_t)s * GB, lane);
+        __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)s * 256, 16), 16);
+      }
+      mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+    }
   } else {
     // Two register sets used in turn: the next column's loads are in flight
     // while the current one is multiplied, with no copies between them.
@@ -368,7 +382,7 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
   return ((rr[0] + rr[16]) + rr[32]) + rr[48];
 }
 
-template <int KIND, int NW, bool PF>
+template <int KIND, int NW, int PIPE>
 __global__ __launch_bounds__(64 * NW) void kq_mv_mfma(const uint8_t* __restrict__ P, int nsb, int out_rows,
                                                      const float* __restrict__ x, float* __restrict__ y, int spw,
                                                      float* __restrict__ part, unsigned* __restrict__ count) {
@@ -376,14 +390,14 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma(const uint8_t* __restrict_
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = blockIdx.x;
-  const float rowsum = mv_mfma_rows<KIND, PF>(P, nsb, tile, (blockIdx.y * NW + w) * spw, spw, x, sh[w].img,
+  const float rowsum = mv_mfma_rows<KIND, PIPE>(P, nsb, tile, (blockIdx.y * NW + w) * spw, spw, x, sh[w].img,
                                               sh[w].xsum, sh[w].hdr.a, lane);
   mv_epilogue<NW>(rowsum, tile, tile, out_rows, y, part, count);
 }
 
 // Two matrices that multiply the same x (q|k and v of attention): tiles
 // [0, tiles_a) of the grid are matrix A's (kind KA), the rest matrix B's.
-template <int KA, int KB, int NW, bool PF>
+template <int KA, int KB, int NW, int PIPE>
 __global__ __launch_bounds__(64 * NW) void kq_mv_mfma2(const uint8_t* __restrict__ Pa, int out_a, float* __restrict__ ya,
                                                       const uint8_t* __restrict__ Pb, int out_b, float* __restrict__ yb,
                                                       int tiles_a, int nsb, const float* __restrict__ x, int spw,
@@ -394,11 +408,11 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma2(const uint8_t* __restrict
   const int gtile = blockIdx.x;
   const int sb0 = (blockIdx.y * NW + w) * spw;
   if (gtile < tiles_a) {
-    const float r = mv_mfma_rows<KA, PF>(Pa, nsb, gtile, sb0, spw, x, sh[w].img, sh[w].xsum, sh[w].hdr.a, lane);
+    const float r = mv_mfma_rows<KA, PIPE>(Pa, nsb, gtile, sb0, spw, x, sh[w].img, sh[w].xsum, sh[w].hdr.a, lane);
     mv_epilogue<NW>(r, gtile, gtile, out_a, ya, part, count);
   } else {
     const float r =
-        mv_mfma_rows<KB, PF>(Pb, nsb, gtile - tiles_a, sb0, spw, x, sh[w].img, sh[w].xsum, sh[w].hdr.b, lane);
+        mv_mfma_rows<KB, PIPE>(Pb, nsb, gtile - tiles_a, sb0, spw, x, sh[w].img, sh[w].xsum, sh[w].hdr.b, lane);
     mv_epilogue<NW>(r, gtile, gtile - tiles_a, out_b, yb, part, count);
   }
 }
@@ -410,34 +424,31 @@ void set_matvec_engine(int engine) { g_engine = engine; }
 
 bool matvec_mfma_takes(int kind) { return (kind == Q4_K || kind == Q6_K) && g_engine.load() == 0; }
 
+// The kernel a plan runs: NW waves per workgroup and the column walk.
+static int mv_pipe(const PackedPlan& p) { return p.spw == 1 ? MV_ONE : p.seq ? MV_SEQ : MV_PF; }
+
 template <int KIND>
 static hipError_t launch_mfma_kind(const uint8_t* w, int in_dim, int out_dim, const float* x, float* y, float* part,
                                    unsigned* count, hipStream_t s) {
   const PackedPlan p = mfma_plan(KIND, in_dim, out_dim);
   const dim3 grid((out_dim + 63) / 64, p.ks);
-  const int nsb = in_dim / 256;
-  switch (p.nw) {
-#define KQ_MVM(N)                                                                                                   \
-  case N:                                                                                                           \
-    if (p.spw > 1) {                                                                                                \
-      if constexpr (N < 8 || KIND != Q6_K)                                                                          \
-        hipLaunchKernelGGL((kq_mv_mfma<KIND, N, true>), grid, dim3(64 * N), 0, s, w, nsb, out_dim, x, y, p.spw,     \
-                           part, count);                                                                            \
-      else                                                                                                          \
-        return hipErrorInvalidValue; /* Q6_K's prefetching waves: at most 4 per workgroup */                       \
-    } else                                                                                                          \
-      hipLaunchKernelGGL((kq_mv_mfma<KIND, N, false>), grid, dim3(64 * N), 0, s, w, nsb, out_dim, x, y, p.spw,      \
-                         part, count);                                                                              \
+  const int nsb = in_dim / 256, pipe = mv_pipe(p);
+#define KQ_GO(N, PIPE) \
+  hipLaunchKernelGGL((kq_mv_mfma<KIND, N, PIPE>), grid, dim3(64 * N), 0, s, w, nsb, out_dim, x, y, p.spw, part, count)
+#define KQ_NW(N)                                                                                \
+  case N:                                                                                       \
+    if (pipe == MV_ONE) KQ_GO(N, MV_ONE);                                                       \
+    else if constexpr (N == 16) return hipErrorInvalidValue; /* 16 waves: one column only */    \
+    else if (pipe == MV_SEQ) KQ_GO(N, MV_SEQ);                                                  \
+    else if constexpr (N <= 4 || (N == 8 && KIND != Q6_K)) KQ_GO(N, MV_PF);                     \
+    else return hipErrorInvalidValue; /* two register sets: <= 8 waves per group, 4 for Q6_K */ \
     break;
-    case 16:  // one column per wave only (the register file holds 16 such waves)
-      if (p.spw != 1) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((kq_mv_mfma<KIND, 16, false>), grid, dim3(1024), 0, s, w, nsb, out_dim, x, y, p.spw, part,
-                         count);
-      break;
-    KQ_MVM(8) KQ_MVM(4) KQ_MVM(2) KQ_MVM(1)
-#undef KQ_MVM
+  switch (p.nw) {
+    KQ_NW(16) KQ_NW(8) KQ_NW(4) KQ_NW(2) KQ_NW(1)
     default: return hipErrorInvalidValue;
   }
+#undef KQ_NW
+#undef KQ_GO
   return hipGetLastError();
 }
 
@@ -448,31 +459,27 @@ static hipError_t launch_mfma_pair(const uint8_t* a, int out_a, float* ya, const
                                    int in_dim, const float* x, float* part, unsigned* count, hipStream_t s) {
   const int tiles_a = (out_a + 63) / 64, tiles_b = (out_b + 63) / 64;
   // The split of the wider kind's registers (Q6_K when either is).
-  const PackedPlan p = mfma_plan(KA == Q6_K || KB == Q6_K ? Q6_K : Q4_K, in_dim, (tiles_a + tiles_b) * 64);
+  constexpr int KW = KA == Q6_K || KB == Q6_K ? Q6_K : Q4_K;
+  const PackedPlan p = mfma_plan(KW, in_dim, (tiles_a + tiles_b) * 64);
   const dim3 grid(tiles_a + tiles_b, p.ks);
-  const int nsb = in_dim / 256;
-  switch (p.nw) {
-#define KQ_MVM2(N)                                                                                                   \
-  case N:                                                                                                            \
-    if (p.spw > 1) {                                                                                                 \
-      if constexpr (N < 8 || (KA != Q6_K && KB != Q6_K))                                                             \
-        hipLaunchKernelGGL((kq_mv_mfma2<KA, KB, N, true>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb,     \
-                           tiles_a, nsb, x, p.spw, part, count);                                                     \
-      else                                                                                                           \
-        return hipErrorInvalidValue; /* Q6_K's prefetching waves: at most 4 per workgroup */                        \
-    } else                                                                                                           \
-      hipLaunchKernelGGL((kq_mv_mfma2<KA, KB, N, false>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb,      \
-                         tiles_a, nsb, x, p.spw, part, count);                                                       \
+  const int nsb = in_dim / 256, pipe = mv_pipe(p);
+#define KQ_GO(N, PIPE)                                                                                            \
+  hipLaunchKernelGGL((kq_mv_mfma2<KA, KB, N, PIPE>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb, tiles_a, \
+                     nsb, x, p.spw, part, count)
+#define KQ_NW(N)                                                          \
+  case N:                                                                 \
+    if (pipe == MV_ONE) KQ_GO(N, MV_ONE);                                 \
+    else if constexpr (N == 16) return hipErrorInvalidValue;              \
+    else if (pipe == MV_SEQ) KQ_GO(N, MV_SEQ);                            \
+    else if constexpr (N <= 4 || (N == 8 && KW != Q6_K)) KQ_GO(N, MV_PF); \
+    else return hipErrorInvalidValue;                                     \
     break;
-    case 16:  // one column per wave only
-      if (p.spw != 1) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((kq_mv_mfma2<KA, KB, 16, false>), grid, dim3(1024), 0, s, a, out_a, ya, b, out_b, yb, tiles_a,
-                         nsb, x, p.spw, part, count);
-      break;
-    KQ_MVM2(8) KQ_MVM2(4) KQ_MVM2(2) KQ_MVM2(1)
-#undef KQ_MVM2
+  switch (p.nw) {
+    KQ_NW(16) KQ_NW(8) KQ_NW(4) KQ_NW(2) KQ_NW(1)
     default: return hipErrorInvalidValue;
   }
+#undef KQ_NW
+#undef KQ_GO
   return hipGetLastError();
 }
 

@@ -151,13 +151,16 @@ void set_packed_plan_override(int nw, int ks) {
   g_plan_ks = ks;
 }
 
+int packed_plan_override_ks() { return g_plan_ks; }
+
 PackedPlan packed_plan(int in_dim, int out_dim) {
   static const int cus = device_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   PackedPlan p{1, 1, nsb};
   {
     const int onw = g_plan_nw, oks = g_plan_ks;
-    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && onw <= 16 && nsb % (onw * oks) == 0) {
+    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && nsb % (onw * oks) == 0 &&
+      (onw <= 8 || (onw == 16 && nsb == onw * oks))) {
       p.nw = onw;
       p.ks = oks;
       p.spw = nsb / (onw * oks);
@@ -201,41 +204,50 @@ PackedPlan packed_plan(int in_dim, int out_dim) {
 
 // Split of the MFMA matvec (kq_mv_mfma.hip), fitted to measurements on
 // MI355X at the Llama-3-8B Q4_K_M shapes (launch time per split, cold HBM):
-//   * a tile per CU or more, 16 columns: whole tiles by 16 one-column waves (no
-//     cross-workgroup sum, whose atomic round trip holds every workgroup ~1 us
-//     longer; 28672x4096: 15.3 us against 16.4 for 4 workgroups per tile),
-//     or 8-wave halves once the tiles are 4 per CU (128256x4096: 80 us
-//     against 82);
-//   * a tile per CU or more, other widths: whole tiles by up to 8 waves (4 for
-//     Q6_K, whose prefetching waves hold ~260 registers) of several columns;
+//   * a tile per CU or more: whole tiles (no cross-workgroup sum, whose atomic
+//     round trip holds every workgroup ~1 us longer) by 4 waves, each taking
+//     its columns one after another with one register set (~140 registers,
+//     3 workgroups per CU, so all tiles run in one round): 28672x4096 14.5 us
+//     against 15.3 for 16 one-column waves and 16.2 for 4 groups per tile;
+//     128256x4096 75.7 us against 81;
 //   * narrower matrices: one column per wave, the most waves per workgroup
 //     (<= 8) that still leave >= 150 workgroups, at least 2 (4096x14336 Q6_K
-//     8 x 7 groups: 12.5 us against 14.5 for 4 x 14; 4096x4096: 4 x 4;
+//     8 x 7 groups: 12.6 us against 14.1 for 4 x 14; 4096x4096: 4 x 4, 5.5 us;
 //     1024x4096: 2 x 8).
+static std::atomic<int> g_mfma_pipe{0};
+
+void set_mfma_pipeline(int mode) { g_mfma_pipe = mode; }
+
+static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim);
+
 PackedPlan mfma_plan(int kind, int in_dim, int out_dim) {
+  const int nsb = in_dim / 256;
+  const int pipe = g_mfma_pipe;
+  PackedPlan p = mfma_plan_choice(kind, in_dim, out_dim);
+  const int onw = g_plan_nw, oks = g_plan_ks;
+  if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && nsb % (onw * oks) == 0 &&
+      (onw <= 8 || (onw == 16 && nsb == onw * oks))) {
+    p.nw = onw;
+    p.ks = oks;
+    p.spw = nsb / (onw * oks);
+    p.seq = false;
+  }
+  if (pipe == 1) p.seq = false;
+  if (pipe == 2) p.seq = true;
+  // Prefetching waves (two register sets) fit at most 8 per workgroup, 4 for Q6_K.
+  if (p.spw > 1 && !p.seq && p.nw > (kind == Q6_K ? 4 : 8)) p.seq = true;
+  return p;
+}
+
+static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   static const int cus = device_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   PackedPlan p{1, 1, nsb};
-  {
-    const int onw = g_plan_nw, oks = g_plan_ks;
-    if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && nsb % (onw * oks) == 0 &&
-        (onw <= 8 || (onw == 16 && nsb == onw * oks))) {
-      p.nw = onw;
-      p.ks = oks;
-      p.spw = nsb / (onw * oks);
-      return p;
-    }
-  }
   if (ntiles >= cus) {
-    if (nsb == 16) {
-      p.spw = 1;
-      p.nw = ntiles >= 4 * cus ? 8 : 16;
-      p.ks = nsb / p.nw;
-      return p;
-    }
     p.ks = 1;
-    p.nw = pow2_divisor_upto(nsb, kind == Q6_K ? 4 : 8);
+    p.nw = pow2_divisor_upto(nsb, 4);
     p.spw = nsb / p.nw;
+    p.seq = true;
     return p;
   }
   p.spw = 1;

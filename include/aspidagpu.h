@@ -106,7 +106,9 @@ int aspida_kq_unpack_dev(int kind, const void *packed, int in_dim, int out_dim, 
  * tile and super-block columns per wave (their product is in_dim / 256). */
 /* The kernel and split aspida_kq_matvec_packed_dev uses for a kind and shape
  * under the current engine (aspida_kq_set_mv_engine): returns 1 for the
- * matrix-core kernel kq_mv_mfma<kind, waves, prefetch>, 0 for the vector kernel
+ * matrix-core kernel kq_mv_mfma<kind, waves, prefetch> (prefetch = columns
+ * per wave > 1), 2 for the same kernel taking its columns one after another
+ * (kq_mv_mfma<kind, waves, false>), 0 for the vector kernel
  * kq_mv_packed<kind, waves, prefetch>, or -EINVAL.  No reference counterpart. */
 int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int *waves_per_group, int *groups_per_tile,
                           int *columns_per_wave);
@@ -285,6 +287,24 @@ int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile);
  * Process-wide; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mv_engine(int engine);
+
+/* Engine of the packed small-batch product (batch > 1 in
+ * aspida_kq_matmul_packed_dev and aspida_gpu_matmul): 0 = the built-in choice
+ * (Q4_K and Q6_K up to 4 vectors on the vector kernel, then Q4_K on the
+ * 16-vector matrix-core kernel -- above 16 vectors only for matrices of at
+ * least 2048 64-row-by-256-column blocks, else the 64-vector one -- and Q6_K
+ * on the 64-vector matrix-core kernel; other kinds on the vector kernel); 1 = the
+ * vector kernel; 2 = the 64-vector and 3 = the 16-vector matrix-core kernel
+ * for the kinds that have one (others stay on the vector kernel).
+ * Process-wide; for comparison and tests.  No reference counterpart.
+ * Returns 0, or -EINVAL for another value. */
+int aspida_kq_set_mm_engine(int engine);
+
+/* Tuning of the matrix-core matvec's splits with several columns per wave:
+ * 0 = the built-in choice, 1 = prefetching waves (two register sets),
+ * 2 = columns one after another (one register set, more waves per CU).
+ * Process-wide.  No reference counterpart.  Returns 0 or -EINVAL. */
+int aspida_kq_set_mfma_pipeline(int mode);
 
 /* Launch-shape override for batch-1 matvecs: rows per lane group per step
  * (1, 2 or 4) and resident waves launched per CU (1..64); rows_per_wave <= 0

@@ -92,11 +92,13 @@ def _packed_rows(kind, w, X, in_dim, out_dim):
     return np.stack(out)
 
 
-# Multi-vector VALU product (up to 4 rows for Q4_K/Q6_K, 8 for the other
-# kinds; rows bit-identical to the batch-1 kernel): ragged weight rows, one
-# super-block column, tiles split over workgroups (ks > 1), columns per wave
-# > 1.  Q4_K/Q6_K batches of 5 and 8 go to MFMA and are checked row by row.
-MULTI_CASES = [(2, 130, 768), (3, 1000, 4096), (4, 64, 14336), (5, 64, 14336), (8, 300, 256), (8, 4096, 4096)]
+# Multi-vector VALU product (the small-batch engine of the kinds without an
+# MFMA kernel; forced here for Q4_K/Q6_K too): rows bit-identical to the
+# batch-1 VALU kernel.  Ragged weight rows, one super-block column, tiles
+# split over workgroups (ks > 1), columns per wave > 1, batches of 8 and one
+# beyond (two launches).
+MULTI_CASES = [(2, 130, 768), (3, 1000, 4096), (4, 64, 14336), (5, 64, 14336), (8, 300, 256), (8, 4096, 4096),
+               (11, 200, 1024)]
 
 
 @pytest.mark.parametrize("case", MULTI_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
@@ -106,13 +108,12 @@ def test_multi_vector_rows_bit_identical_to_matvec(kind, case):
     gen = synth.rng(700 + batch + kind * 7 + out_dim)
     w = synth.weight_np(kind, out_dim, in_dim, gen)
     X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
-    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
-    if kind in (aa.Q4_K, aa.Q6_K) and batch > 4:
-        # served by the MFMA kernel: every row against the oracle instead
-        for b in range(batch):
-            want = oracle.qmatvec(kind, w, in_dim, out_dim, X[b], nthreads=ncpu())
-            assert_close_scaled(Y[b], want, abs_dot_scale(kind, w, in_dim, out_dim, X[b]), what=f"row {b}")
-        return
+    dev = aa.DeviceOps()
+    dev.set_mm_engine(1)
+    try:
+        Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    finally:
+        dev.set_mm_engine(0)
     R = _packed_rows(kind, w, X, in_dim, out_dim)
     assert np.array_equal(Y.view(np.uint32), R.view(np.uint32)), "rows differ from the batch-1 kernel"
     want = oracle.qmatvec(kind, w, in_dim, out_dim, X[-1], nthreads=ncpu())
@@ -149,6 +150,33 @@ def test_mfma_matmul_matches_oracle(kind, case):
     want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
     assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
                         what=f"{aa.KIND_NAMES[kind]} B={batch} {out_dim}x{in_dim}")
+
+
+# Every small-batch engine on the Q4_K product (aspida_kq_set_mm_engine: the
+# vector kernel, the 64-vector and the 16-vector MFMA kernels): batches below,
+# at and above 16 (two 16-vector launches, one ragged), ragged weight rows,
+# one column per wave and long column runs, tiles split over workgroups.
+MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304), (40, 4096, 4096),
+                   (9, 16448, 2048), (3, 256, 14336)]
+
+
+@pytest.mark.parametrize("engine", [1, 2, 3])
+@pytest.mark.parametrize("case", MM_ENGINE_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
+def test_mm_engines_match_oracle(case, engine):
+    kind = aa.Q4_K
+    batch, out_dim, in_dim = case
+    gen = synth.rng(950 + batch + out_dim)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    dev = aa.DeviceOps()
+    dev.set_mm_engine(engine)
+    try:
+        Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    finally:
+        dev.set_mm_engine(0)
+    want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
+    assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
+                        what=f"engine {engine} B={batch} {out_dim}x{in_dim}")
 
 
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K])
