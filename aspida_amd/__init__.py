@@ -81,6 +81,7 @@ def load(path=None):
         "aspida_kq_chain_destroy": (None, [P]),
         "aspida_kq_set_packed_plan": (I, [I, I]),
         "aspida_kq_set_mv_engine": (I, [I]),
+        "aspida_kq_set_mfma_rows": (I, [I]),
         "aspida_kq_set_mm_engine": (I, [I]),
         "aspida_kq_set_mfma_pipeline": (I, [I]),
         "aspida_kq_set_mv_config": (I, [I, I]),
@@ -193,13 +194,14 @@ class DeviceOps:
 
     def matvec_plan(self, kind, in_dim, out_dim):
         """(uses the MFMA kernel, waves per workgroup, workgroups per tile,
-        columns per wave, columns taken one after another) of
+        columns per wave, columns taken one after another, 16-row
+        workgroups) of
         aspida_kq_matvec_packed_dev for this kind."""
         v = [ctypes.c_int(0) for _ in range(3)]
         rc = self.lib.aspida_kq_matvec_plan(kind, in_dim, out_dim, *[ctypes.byref(a) for a in v])
         if rc < 0:
             raise RuntimeError(f"aspida_kq_matvec_plan failed with code {rc}")
-        return (rc >= 1,) + tuple(a.value for a in v) + (rc == 2,)
+        return (rc >= 1,) + tuple(a.value for a in v) + (rc in (2, 4), rc >= 3)
 
     def pack(self, kind, w, in_dim, out_dim, packed, stream=0):
         self._ok(self.lib.aspida_kq_pack_dev(kind, w, in_dim, out_dim, packed, stream), "aspida_kq_pack_dev")
@@ -273,6 +275,10 @@ class DeviceOps:
     def set_mv_engine(self, engine):
         """0: MFMA for Q4_K and Q6_K (default), 1: the VALU kernel for every kind."""
         self._ok(self.lib.aspida_kq_set_mv_engine(engine), "aspida_kq_set_mv_engine")
+
+    def set_mfma_rows(self, mode):
+        """Matrix-core matvec workgroups: 0 built-in choice, 1 64-row, 2 16-row."""
+        self._ok(self.lib.aspida_kq_set_mfma_rows(mode), "aspida_kq_set_mfma_rows")
 
     def set_mm_engine(self, engine):
         """Batches > 1: 0 built-in choice, 1 VALU, 2 64-vector MFMA, 3 16-vector MFMA."""

@@ -563,7 +563,9 @@ extern "C" int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int* wav
   *waves_per_group = p.nw;
   *groups_per_tile = p.ks;
   *columns_per_wave = p.spw;
-  return mfma ? (p.seq && p.spw > 1 ? 2 : 1) : 0;
+  if (!mfma) return 0;
+  const int seq = p.seq && p.spw > 1 ? 1 : 0;
+  return p.blk16 ? 3 + seq : 1 + seq;
 }
 
 extern "C" int aspida_kq_pack_dev(int kind, const void* w, int in_dim, int out_dim, void* packed, void* stream) {
@@ -817,6 +819,12 @@ extern "C" int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_til
 extern "C" int aspida_kq_set_mfma_pipeline(int mode) {
   if (mode < 0 || mode > 2) return -EINVAL;
   kq::set_mfma_pipeline(mode);
+  return 0;
+}
+
+extern "C" int aspida_kq_set_mfma_rows(int mode) {
+  if (mode < 0 || mode > 2) return -EINVAL;
+  kq::set_mfma_rows(mode);
   return 0;
 }
 

@@ -42,11 +42,14 @@ hipError_t launch_dequant(int kind, const void* W, int in_dim, int out_dim, floa
 // per workgroup, ks workgroups per 64-row tile (nw * ks * spw == in_dim / 256).
 struct PackedPlan {
   int nw, ks, spw;
-  bool seq = false;  // MFMA kernel: columns one after another (one register set) even when spw > 1
+  bool seq = false;    // MFMA kernel: columns one after another (one register set) even when spw > 1
+  bool blk16 = false;  // MFMA kernel: 16-row workgroups over all columns (nw waves, spw columns each, ks = 1)
 };
 PackedPlan packed_plan(int in_dim, int out_dim);
 // The split of the MFMA matvec (kq_mv_mfma.hip) for a kind.
 PackedPlan mfma_plan(int kind, int in_dim, int out_dim);
+// Tuning: 0 = the plan's choice, 1 = 64-row workgroups, 2 = 16-row workgroups.
+void set_mfma_rows(int mode);
 // Tuning: 0 = the plan's choice, 1 = prefetching waves, 2 = sequential columns
 // (for splits with more than one column per wave).
 void set_mfma_pipeline(int mode);

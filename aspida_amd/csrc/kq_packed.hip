@@ -218,12 +218,45 @@ static std::atomic<int> g_mfma_pipe{0};
 
 void set_mfma_pipeline(int mode) { g_mfma_pipe = mode; }
 
+static std::atomic<int> g_mfma_rows{0};
+
+void set_mfma_rows(int mode) { g_mfma_rows = mode; }
+
+// 16-row workgroups (kq_mv_mfma16): as many waves as divide the columns, up
+// to 16 (the instantiated counts), several columns per wave taken one after
+// another (measured faster than prefetching on MI355X).
+static PackedPlan mfma16_plan(int nsb) {
+  PackedPlan p{1, 1, nsb};
+  for (int n : {16, 14, 8, 4, 2, 1})
+    if (nsb % n == 0) {
+      p.nw = n;
+      break;
+    }
+  p.spw = nsb / p.nw;
+  p.seq = p.spw > 1;
+  p.blk16 = true;
+  return p;
+}
+
 static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim);
+static PackedPlan mfma64_plan(int kind, int in_dim, int out_dim);
 
 PackedPlan mfma_plan(int kind, int in_dim, int out_dim) {
   const int nsb = in_dim / 256;
-  const int pipe = g_mfma_pipe;
+  const int pipe = g_mfma_pipe, rows = g_mfma_rows;
   PackedPlan p = mfma_plan_choice(kind, in_dim, out_dim);
+  if (rows == 2 || (rows == 0 && p.blk16)) {
+    p = mfma16_plan(nsb);
+    const int onw = g_plan_nw;
+    if ((onw == 16 || onw == 14 || onw == 8 || onw == 4 || onw == 2 || onw == 1) && nsb % onw == 0) {
+      p.nw = onw;
+      p.spw = nsb / onw;
+    }
+    if (pipe == 1) p.seq = false;
+    if (pipe == 2) p.seq = p.spw > 1;
+    return p;
+  }
+  if (p.blk16) p = mfma64_plan(kind, in_dim, out_dim);
   const int onw = g_plan_nw, oks = g_plan_ks;
   if (onw > 0 && oks > 0 && (onw & (onw - 1)) == 0 && nsb % (onw * oks) == 0 &&
       (onw <= 8 || (onw == 16 && nsb == onw * oks))) {
@@ -241,6 +274,20 @@ PackedPlan mfma_plan(int kind, int in_dim, int out_dim) {
 
 static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   static const int cus = device_cus();
+  const int ntiles = (out_dim + 63) / 64;
+  // The 16-row kernels (no partial sums through memory) for up to two 16-row
+  // blocks per CU, when a wave takes at most one column or the blocks fill
+  // every CU (otherwise few CUs would walk long column runs).  Measured on
+  // MI355X: Q4_K 4096x4096 4.3 us against 5.8 us on 64-row workgroups with
+  // partial sums; 1024x14336 5.9 us on 64-row workgroups against 8.1 us.
+  const int nsb = in_dim / 256;
+  if (4L * ntiles <= 2L * cus && (nsb <= 16 || 4L * ntiles >= cus)) return mfma16_plan(nsb);
+  return mfma64_plan(kind, in_dim, out_dim);
+}
+
+static PackedPlan mfma64_plan(int kind, int in_dim, int out_dim) {
+  (void)kind;
+  static const int cus = device_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   PackedPlan p{1, 1, nsb};
   if (ntiles >= cus) {
@@ -251,6 +298,13 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
     return p;
   }
   p.spw = 1;
+  if (2L * ntiles >= cus && nsb <= 16 && (nsb & (nsb - 1)) == 0) {
+    // A tile per workgroup and a column per wave: no partial sums (Q4_K
+    // 14336x4096: 8.6 us against 9.8 us with two workgroups per tile).
+    p.nw = nsb;
+    p.ks = 1;
+    return p;
+  }
   int nw = pow2_divisor_upto(nsb, 8);
   while (nw > 2 && (long)ntiles * (nsb / nw) < 150) nw /= 2;
   p.nw = nw;

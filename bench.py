@@ -158,22 +158,23 @@ def mfma_walk(spw, seq):
 def kernel_name(dec, op):
     """The kernel symbol a launch runs: kq_mv_mfma<kind, waves, walk> and
     kq_mv_mfma2<kind_a, kind_b, waves, walk> (Q4_K and Q6_K on the matrix
-    cores), kq_mv_packed<kind, waves, prefetch> or
+    cores; kq_mv_mfma16 / kq_mv_mfma2_16 on 16-row workgroups),
+    kq_mv_packed<kind, waves, prefetch> or
     kq_mv_packed2<kind_a, kind_b, waves, prefetch> (the launch split is the
     library's: aspida_kq_matvec_plan, aspida_kq_packed_plan)."""
     rows = sum(-(-o // 64) * 64 for _, _, _, o, _, _ in op)
     kinds = [m[0] for m in op]
     if len(op) == 1:
-        mfma, nw, _, spw, seq = dec.dev.matvec_plan(kinds[0], op[0][2], rows)
+        mfma, nw, _, spw, seq, b16 = dec.dev.matvec_plan(kinds[0], op[0][2], rows)
         if mfma:
-            return f"kq_mv_mfma<{kinds[0]}, {nw}, {mfma_walk(spw, seq)}>"
+            return f"kq_mv_mfma{'16' if b16 else ''}<{kinds[0]}, {nw}, {mfma_walk(spw, seq)}>"
     else:
         aa = dec.aa
         # the pair runs on MFMA when both kinds do, with the wider kind's split
         mf = [dec.dev.matvec_plan(k, op[0][2], rows) for k in kinds]
         if all(m[0] for m in mf):
-            _, nw, _, spw, seq = dec.dev.matvec_plan(aa.Q6_K if aa.Q6_K in kinds else kinds[0], op[0][2], rows)
-            return f"kq_mv_mfma2<{kinds[0]}, {kinds[1]}, {nw}, {mfma_walk(spw, seq)}>"
+            _, nw, _, spw, seq, b16 = dec.dev.matvec_plan(aa.Q6_K if aa.Q6_K in kinds else kinds[0], op[0][2], rows)
+            return f"kq_mv_mfma2{'_16' if b16 else ''}<{kinds[0]}, {kinds[1]}, {nw}, {mfma_walk(spw, seq)}>"
         nw, _, spw = dec.dev.packed_plan(op[0][2], rows)
     pf = "true" if spw > 1 else "false"
     kinds = ", ".join(str(m[0]) for m in op)

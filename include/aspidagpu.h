@@ -106,9 +106,11 @@ int aspida_kq_unpack_dev(int kind, const void *packed, int in_dim, int out_dim, 
  * tile and super-block columns per wave (their product is in_dim / 256). */
 /* The kernel and split aspida_kq_matvec_packed_dev uses for a kind and shape
  * under the current engine (aspida_kq_set_mv_engine): returns 1 for the
- * matrix-core kernel kq_mv_mfma<kind, waves, prefetch> (prefetch = columns
- * per wave > 1), 2 for the same kernel taking its columns one after another
- * (kq_mv_mfma<kind, waves, false>), 0 for the vector kernel
+ * matrix-core kernel on 64-row workgroups kq_mv_mfma<kind, waves, walk> (walk
+ * 0: one column per wave, 1: prefetching columns), 2 for the same kernel
+ * taking its columns one after another (walk 2), 3 and 4 for the same two
+ * walks of the 16-row-workgroup kernel kq_mv_mfma16<kind, waves, walk>
+ * (groups_per_tile is then 1), 0 for the vector kernel
  * kq_mv_packed<kind, waves, prefetch>, or -EINVAL.  No reference counterpart. */
 int aspida_kq_matvec_plan(int kind, int in_dim, int out_dim, int *waves_per_group, int *groups_per_tile,
                           int *columns_per_wave);
@@ -299,6 +301,13 @@ int aspida_kq_set_mv_engine(int engine);
  * Process-wide; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mm_engine(int engine);
+
+/* Workgroup shape of the matrix-core matvec: 0 = the built-in choice (16-row
+ * workgroups over all columns for matrices of up to two such blocks per
+ * compute unit, 64-row workgroups above), 1 = 64-row, 2 = 16-row workgroups.
+ * Process-wide; for tuning and tests.  No reference counterpart.
+ * Returns 0 or -EINVAL. */
+int aspida_kq_set_mfma_rows(int mode);
 
 /* Tuning of the matrix-core matvec's splits with several columns per wave:
  * 0 = the built-in choice, 1 = prefetching waves (two register sets),

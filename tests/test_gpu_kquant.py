@@ -382,3 +382,38 @@ def test_engines_activation_range(kind, engine, dev):
                 print(f"  max err / sum|wx| = {r:.2e}", flush=True)
     finally:
         dev.set_mv_engine(0)
+
+
+# Matrix-core matvec workgroup shapes forced (aspida_kq_set_mfma_rows: 64-row
+# workgroups with partial sums across workgroups, 16-row workgroups over all
+# columns) and column walks (one column, prefetching, one after another):
+# ragged rows, a single 16-row block, long column runs, both pair kernels.
+MFMA_SHAPE_CASES = [(64, 4096), (130, 4096), (1000, 2048), (4096, 4096), (300, 14336), (4096, 14336), (16448, 4096),
+                    (37, 256)]
+
+
+@pytest.mark.parametrize("pipe", [0, 1, 2], ids=["plan", "prefetch", "sequential"])
+@pytest.mark.parametrize("rows", [1, 2], ids=["rows64", "rows16"])
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+def test_mfma_workgroup_shapes(kind, rows, pipe, dev):
+    dev.set_mfma_rows(rows)
+    dev.lib.aspida_kq_set_mfma_pipeline(pipe)
+    try:
+        for i, (out_dim, in_dim) in enumerate(MFMA_SHAPE_CASES):
+            plan = dev.matvec_plan(kind, in_dim, out_dim)
+            assert plan[0] and plan[5] == (rows == 2), plan
+            _check_dev(dev, kind, out_dim, in_dim, 5100 + 10 * i + kind, "packed",
+                       f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} rows={rows} pipe={pipe} plan={plan}")
+    finally:
+        dev.set_mfma_rows(0)
+        dev.lib.aspida_kq_set_mfma_pipeline(0)
+
+
+@pytest.mark.parametrize("rows", [1, 2], ids=["rows64", "rows16"])
+@pytest.mark.parametrize("case", PAIR_CASES[:5], ids=lambda c: f"{aa.KIND_NAMES[c[0]]}{c[1]}_{aa.KIND_NAMES[c[2]]}{c[3]}_{c[4]}")
+def test_packed_matvec_pair_workgroup_shapes(case, rows, dev):
+    dev.set_mfma_rows(rows)
+    try:
+        test_packed_matvec_pair(case, dev)
+    finally:
+        dev.set_mfma_rows(0)
