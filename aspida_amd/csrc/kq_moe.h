@@ -56,19 +56,24 @@ struct MoeGroupedArgs {
   const float* x;        // [T][dim], 16-byte aligned rows
   const float* sgi;      // shared gate input [dim] or null
   float *h, *yk, *gsh, *y;
-  unsigned* count;       // [T][tiles_dim] arrival counters, one per 256 bytes
-  int T, top_k, n_exp, dim, I, tiles_dim;
+  unsigned* count;       // [T][blocks_dim] arrival counters, one per 256 bytes
+  int T, top_k, n_exp, dim, I;
+  int tiles_dim;         // 64-row tiles of dim (vector-ALU down projection)
+  int blocks_dim;        // 16-row blocks of dim (matrix-core down projection)
 };
 
 size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k);
 // Points h, yk, gsh, count into `work` (moe_grouped_work_bytes of a.T, a.dim,
-// a.I, a.top_k, 256-byte aligned) and sets tiles_dim.  The counters need no
+// a.I, a.top_k, 256-byte aligned) and sets tiles_dim, blocks_dim.  The counters need no
 // clearing: the gate/up launch zeroes them.
 void moe_grouped_bind(MoeGroupedArgs& a, void* work);
 bool moe_grouped_supported(int dim, int I, int T, int top_k);
 bool moe_grouped_experts_ok(int n_exp);
 // Two launches: gate/up + SwiGLU, then down + combine (gate and up of one
 // kind, down of another; the shared expert's kinds equal the routed ones).
+// Q4_K and Q6_K projections run on the matrix cores (16-row blocks), the
+// other kinds -- and every kind under aspida_kq_set_mv_engine(1) -- on the
+// vector ALUs (64-row tiles).
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
 
 // Router: logits[t] = router_w[n_exp][dim] . x[t] (f32), stable softmax,

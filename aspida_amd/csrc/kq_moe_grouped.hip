@@ -27,7 +27,9 @@
 #include <map>
 #include <mutex>
 
+#include "kq_kernels.h"
 #include "kq_moe.h"
+#include "kq_mv_mfma.h"
 #include "kq_packed.h"
 
 namespace kq {
@@ -134,20 +136,15 @@ constexpr int moe_gu_waves(int kind, int nw) {
   return (kind == Q6_K || kind == Q8_0 || nw < 4) ? 1 : nw / 2;
 }
 
-template <int KIND, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_waves(KIND, NW)))) void moe_gate_up(MoeGroupedArgs a, int cpw, const float* __restrict__ x,
-                                                      float* __restrict__ h) {
-  __shared__ MoeSched S;
-  __shared__ float part[MOE_JPW][NW][2][64];
-  __shared__ __attribute__((aligned(16))) float xst[NW][256];
-  const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int slots = a.top_k + 1, ne = a.n_exp + 1, tiles = a.I / 64;
-  // Housekeeping for the down launch: zero its arrival counters, and the
-  // shared-expert gate g_t = sigmoid(shared_gate_inp . x_t) (one wave per token).
+// Housekeeping for the down launch, done by the gate/up launch: zero its
+// arrival counters (workgroup 0), and the shared-expert gate
+// g_t = sigmoid(shared_gate_inp . x_t) (llm_moe.adb:285-293), one wave per
+// token.
+__device__ __forceinline__ void moe_gu_prologue(const MoeGroupedArgs& a, const float* __restrict__ x, int nw, int w,
+                                                int lane) {
   if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < a.T * a.tiles_dim; i += blockDim.x) a.count[(size_t)i * COUNTER_STRIDE] = 0u;
-  for (int t = blockIdx.x * NW + w; t < a.T; t += gridDim.x * NW) {
+    for (int i = threadIdx.x; i < a.T * a.blocks_dim; i += blockDim.x) a.count[(size_t)i * COUNTER_STRIDE] = 0u;
+  for (int t = blockIdx.x * nw + w; t < a.T; t += gridDim.x * nw) {
     float s = 0.f;
     if (a.sgi) {
       // dim / 256 float4 per lane, loaded together (dim is a multiple of 256).
@@ -174,6 +171,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_
     }
     if (lane == 0) a.gsh[t] = a.sgi ? 1.0f / (1.0f + expf(-s)) : 1.0f;
   }
+}
+
+template <int KIND, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_waves(KIND, NW)))) void moe_gate_up(MoeGroupedArgs a, int cpw, const float* __restrict__ x,
+                                                      float* __restrict__ h) {
+  __shared__ MoeSched S;
+  __shared__ float part[MOE_JPW][NW][2][64];
+  __shared__ __attribute__((aligned(16))) float xst[NW][256];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slots = a.top_k + 1, ne = a.n_exp + 1, tiles = a.I / 64;
+  moe_gu_prologue(a, x, NW, w, lane);
   const int items = moe_schedule(a.idx, a.T, a.top_k, a.n_exp, S) * tiles;
   constexpr int GB = 64 * Block<KIND>::BYTES;
   const size_t nsb = (size_t)NW * cpw;
@@ -284,10 +293,88 @@ __global__ __launch_bounds__(64 * NW) void moe_down(MoeGroupedArgs a, int cpw, c
   }
 }
 
+// ---- one token on the matrix cores (Q4_K, Q6_K) ---------------------------------
+//
+// With T = 1 each slot is its own expert matrix and the projections are
+// batch-1 matvecs: per wave the 16-row matrix-core matvec's arithmetic
+// (kq_mv_mfma.h: the activation image, MFMA on f16-subnormal codes, scales in
+// f32), with no schedule and no partial sums through memory.
+//   moe_gate_up1  workgroup (slot k, 16-row block b of I): waves [0, NWG) take
+//                 the gate matrix's columns, [NWG, 2 NWG) the up matrix's;
+//                 h[k][16 b + r] = silu(g) u (llm_moe.adb:124-132).
+//                 Workgroup 0 also forms g_t (moe_gu_prologue).
+//   moe_down1     workgroup b (16 rows of dim) takes every (slot, column)
+//                 pair of those rows, NW waves over the pairs, and forms
+//                 y = sum_k top_w[k] y_k (ascending k) + g_t y_shared in LDS
+//                 (llm_moe.adb:270-299).
+// Expert ids outside [0, n_exp) are clamped.
+constexpr int MOE1_MAX_UNITS = 64;  // (slot, down column) pairs per down workgroup
+
+__device__ __forceinline__ int moe_expert(const MoeGroupedArgs& a, int k) {
+  return min(max(a.idx[k], 0), a.n_exp - 1);
+}
+
+template <int KIND, int NWG, int PIPE>
+__global__ __launch_bounds__(128 * NWG) void moe_gate_up1(MoeGroupedArgs a, int cpw) {
+  constexpr int NW = 2 * NWG;
+  __shared__ MvShared16 sh[NW];
+  __shared__ float part[NW][16];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blocks = a.I / 16, k = blockIdx.x / blocks, b = blockIdx.x % blocks;
+  moe_gu_prologue(a, a.x, NW, w, lane);
+  const bool up = w >= NWG;
+  const int wc = up ? w - NWG : w;
+  const uint8_t* M = k < a.top_k ? (up ? a.up : a.gate) + (size_t)moe_expert(a, k) * a.gu_stride
+                                 : (up ? a.sh_up : a.sh_gate);
+  const float r = mv_mfma_rows<KIND, PIPE, 1>(M, a.dim / 256, b >> 2, wc * cpw, cpw, a.x, sh[w].img, sh[w].xsum,
+                                              (MvHdr<KIND>*)nullptr, lane, b & 3);
+  if (lane < 16) part[w][lane] = r;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int q = 0; q < NWG; ++q) {
+      g += part[q][t];
+      u += part[NWG + q][t];
+    }
+    a.h[(size_t)k * a.I + 16 * b + t] = (g / (1.0f + expf(-g))) * u;
+  }
+}
+
+template <int KIND, int NW>
+__global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
+  __shared__ MvShared16 sh[NW];
+  __shared__ float part[MOE1_MAX_UNITS][16];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.x, nsb = a.I / 256, units = (a.top_k + 1) * nsb;
+  for (int u = w; u < units; u += NW) {
+    const int k = u / nsb, c = u % nsb;
+    const uint8_t* M = k < a.top_k ? a.down + (size_t)moe_expert(a, k) * a.d_stride : a.sh_down;
+    const float r = mv_mfma_rows<KIND, MV_ONE, 1>(M, nsb, b >> 2, c, 1, a.h + (size_t)k * a.I, sh[w].img, sh[w].xsum,
+                                                  (MvHdr<KIND>*)nullptr, lane, b & 3);
+    if (lane < 16) part[u][lane] = r;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int t = threadIdx.x;
+    float acc = 0.f;
+    for (int k = 0; k <= a.top_k; ++k) {
+      float s = 0.f;
+      for (int c = 0; c < nsb; ++c) s += part[k * nsb + c][t];
+      acc = acc + (k < a.top_k ? a.top_w[k] : a.gsh[0]) * s;
+    }
+    a.y[16 * b + t] = acc;
+  }
+}
+
 // ---- launchers ------------------------------------------------------------------
 
 // Work layout: h [T][slots][I] | yk [T][slots][dim] | gsh [T] (256-byte
-// rounded) | counters [T][tiles_dim] x COUNTER_STRIDE.  Every part starts on
+// rounded) | counters [T][blocks_dim] x COUNTER_STRIDE (16-row blocks of dim:
+// enough for either down projection).  Every part starts on
 // a 256-byte boundary when work does (I and dim are multiples of 256).
 size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k) {
   const size_t slots = (size_t)top_k + 1;
@@ -295,7 +382,7 @@ size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k) {
   n += (size_t)T * slots * I * 4;                             // h
   n += (size_t)T * slots * dim * 4;                           // yk
   n += ((size_t)T * 4 + 255) / 256 * 256;                     // gsh
-  n += (size_t)T * ((dim + 63) / 64) * COUNTER_STRIDE * 4;    // counters
+  n += (size_t)T * ((dim + 15) / 16) * COUNTER_STRIDE * 4;    // counters
   return n;
 }
 
@@ -310,6 +397,7 @@ void moe_grouped_bind(MoeGroupedArgs& a, void* work) {
   p += ((size_t)a.T * 4 + 255) / 256 * 256;
   a.count = (unsigned*)p;
   a.tiles_dim = (a.dim + 63) / 64;
+  a.blocks_dim = (a.dim + 15) / 16;
 }
 
 // Waves per workgroup for nsb super-block columns: the largest of 8, 4, 3,
@@ -386,7 +474,67 @@ bool moe_grouped_supported(int dim, int I, int T, int top_k) {
 
 bool moe_grouped_experts_ok(int n_exp) { return n_exp > 0 && n_exp <= MOE_MAX_EXP; }
 
+static hipError_t launch_gate_up_valu(const MoeGroupedArgs& a, int gu_kind, hipStream_t s);
+static hipError_t launch_down_valu(const MoeGroupedArgs& a, int down_kind, hipStream_t s);
+
+// One-token launches: gate/up waves per matrix NWG (8, 4, 2 or 1, dividing
+// dim / 256, columns one after another beyond one per wave); down waves up to
+// 16 over the (slot, column) pairs.
+template <int KIND>
+static hipError_t launch_gate_up1_kind(const MoeGroupedArgs& a, hipStream_t s) {
+  const int nsb = a.dim / 256;
+  int nwg = 1;
+  for (int n : {8, 4, 2})
+    if (nsb % n == 0) {
+      nwg = n;
+      break;
+    }
+  const int cpw = nsb / nwg;
+  const dim3 grid((a.top_k + 1) * (a.I / 16));
+#define KQ_GU1(N)                                                                                          \
+  case N:                                                                                                  \
+    if (cpw == 1)                                                                                          \
+      hipLaunchKernelGGL((moe_gate_up1<KIND, N, MV_ONE>), grid, dim3(128 * N), 0, s, a, cpw);            \
+    else                                                                                                   \
+      hipLaunchKernelGGL((moe_gate_up1<KIND, N, MV_SEQ>), grid, dim3(128 * N), 0, s, a, cpw);            \
+    break;
+  switch (nwg) {
+    KQ_GU1(1) KQ_GU1(2) KQ_GU1(4) KQ_GU1(8)
+    default: return hipErrorNotSupported;
+  }
+#undef KQ_GU1
+  return hipGetLastError();
+}
+
+template <int KIND>
+static hipError_t launch_down1_kind(const MoeGroupedArgs& a, hipStream_t s) {
+  const int units = (a.top_k + 1) * (a.I / 256);
+  const int nw = units >= 16 ? 16 : units >= 8 ? 8 : units >= 4 ? 4 : units >= 2 ? 2 : 1;
+  const dim3 grid(a.dim / 16);
+#define KQ_DN1(N) \
+  case N: hipLaunchKernelGGL((moe_down1<KIND, N>), grid, dim3(64 * N), 0, s, a); break;
+  switch (nw) {
+    KQ_DN1(1) KQ_DN1(2) KQ_DN1(4) KQ_DN1(8) KQ_DN1(16)
+    default: return hipErrorNotSupported;
+  }
+#undef KQ_DN1
+  return hipGetLastError();
+}
+
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s) {
+  // One token with matrix-core kinds throughout: the one-token kernels.
+  if (a.T == 1 && matvec_mfma_takes(gu_kind) && matvec_mfma_takes(down_kind) &&
+      (a.top_k + 1) * (a.I / 256) <= MOE1_MAX_UNITS) {
+    const hipError_t e = gu_kind == Q4_K ? launch_gate_up1_kind<Q4_K>(a, s) : launch_gate_up1_kind<Q6_K>(a, s);
+    if (e != hipSuccess) return e;
+    return down_kind == Q4_K ? launch_down1_kind<Q4_K>(a, s) : launch_down1_kind<Q6_K>(a, s);
+  }
+  const hipError_t e = launch_gate_up_valu(a, gu_kind, s);
+  if (e != hipSuccess) return e;
+  return launch_down_valu(a, down_kind, s);
+}
+
+static hipError_t launch_gate_up_valu(const MoeGroupedArgs& a, int gu_kind, hipStream_t s) {
   hipError_t e;
   switch (gu_kind) {
     case Q4_K: e = launch_gate_up_kind<Q4_K>(a, s); break;
@@ -397,7 +545,10 @@ hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kin
     case Q8_0: e = launch_gate_up_kind<Q8_0>(a, s); break;
     default: return hipErrorInvalidValue;
   }
-  if (e != hipSuccess) return e;
+  return e;
+}
+
+static hipError_t launch_down_valu(const MoeGroupedArgs& a, int down_kind, hipStream_t s) {
   switch (down_kind) {
     case Q4_K: return launch_down_kind<Q4_K>(a, s);
     case Q6_K: return launch_down_kind<Q6_K>(a, s);

@@ -1,0 +1,382 @@
+// kq_mv_mfma.h -- the column arithmetic of the matrix-core matvec
+// (kq_mv_mfma.hip), shared with the matrix-core MoE experts (kq_moe16.hip):
+// the per-column activation image, the packed column loads of 16-row blocks,
+// and one column's MFMA dot with its scales.  The layout and accuracy notes
+// are at the top of kq_mv_mfma.hip.
+#pragma once
+#include <algorithm>
+
+#include "kq_packed.h"
+
+namespace kq {
+
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack_f16x2(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ mf4 mfma_f16(uint4 a, uint4 b, mf4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mh8, a), __builtin_bit_cast(mh8, b), c, 0, 0, 0);
+}
+
+// Per-lane constants of one wave.
+struct MvLane {
+  uint32_t* wr_hi;  // this lane's image writes (plane hi; plane lo is the next lane's slot)
+  float odd;        // activation factor of this lane's elements (Q4_K high nibbles: 1/16)
+  bool xs_writer;   // this lane stores a sub-block sum ...
+  int xs_pos;       // ... at this index of the wave's sum array
+  // Q4_K scale extraction for sub-blocks 2g, 2g+1 (get_scale_min_k4,
+  // llm_dequant.adb:514-525): both pairs sit in bytes b0, b0 + 1 of the scale
+  // dwords; g >= 2 takes the low/high nibbles of the third dword plus two bits
+  // from the first/second.
+  bool upper;
+  uint32_t b0, m1, m2, mshift;
+};
+
+// Image slot of A row m = 4 grp + r in lane group grp (the MFMA's lane
+// 16 grp + m = 20 grp + r): the full 64-lane image, or the compact one that
+// keeps only these 16 data lanes (4 grp + r) plus slot 16, always zero, which
+// every other lane reads.
+template <int IL>
+__device__ __forceinline__ constexpr int img_slot(int grp, int r) {
+  return IL == 64 ? 20 * grp + r : 4 * grp + r;
+}
+
+template <int KIND, int IL>
+__device__ __forceinline__ MvLane mv_lane(uint4 (&img)[8][IL], int lane) {
+  MvLane L;
+  const int g = lane >> 4;
+  L.upper = g >= 2;
+  L.b0 = 16u * (uint32_t)(g & 1);
+  L.m1 = L.upper ? 0x0F0Fu : 0x3F3Fu;
+  L.m2 = L.upper ? 0x3030u : 0u;
+  L.mshift = L.b0 + (L.upper ? 4u : 0u);
+  if (KIND == Q4_K) {
+    // Elements 4 lane .. +3 = elements 4 bj .. of sub-block bs: MFMA bj, rows
+    // m = 2 bs (+1) of k-group bs / 2, dwords 2 (bs % 2) + {0, 1}.
+    const int bs = lane >> 3, bj = lane & 7;
+    L.wr_hi = reinterpret_cast<uint32_t*>(&img[bj][img_slot<IL>(bs >> 1, 2 * (bs & 1))]) + 2 * (bs & 1);
+    L.odd = (bs & 1) ? 0.0625f : 1.f;
+    L.xs_writer = bj == 4;  // after the quad sums and row_shr:4
+    L.xs_pos = bs;
+  } else {
+    // Element E = 4 lane = 128 h + 32 k + 16 t + 4 j: quarter c = 2h + t,
+    // MFMA (T = k / 2, j) = image slot 4T + j, rows m = 4c + 2 (k % 2) (+1),
+    // dwords 2 (k % 2) + {0, 1}.  Sub-block E / 16 = 8h + 2k + t, stored at
+    // 4c + k so that lane group c reads its four sums as one float4.
+    const int E = 4 * lane, h = E >> 7, k = (E >> 5) & 3, t = (E >> 4) & 1, j = (E >> 2) & 3;
+    const int c = 2 * h + t;
+    L.wr_hi = reinterpret_cast<uint32_t*>(&img[4 * (k >> 1) + j][img_slot<IL>(c, 2 * (k & 1))]) + 2 * (k & 1);
+    L.odd = 1.f;
+    L.xs_writer = (lane & 3) == 0;  // after the quad sums
+    L.xs_pos = 4 * c + k;
+  }
+  return L;
+}
+
+// Builds the column's A image and sub-block sums of x S from the lane's
+// float4 of x; returns 1/S.
+template <int KIND>
+__device__ __forceinline__ float build_image(float4 xv, const MvLane& L, float* xsum) {
+  float mx = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
+  mx = wave_max(mx);
+  int e = 0;
+  const bool scaled = mx > 0.f && __builtin_isfinite(mx);
+  if (scaled) (void)frexpf(mx, &e);
+  const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
+  const float S = ldexpf(1.f, se);
+  const float sl = S * L.odd;
+  const float v0 = xv.x * sl, v1 = xv.y * sl, v2 = xv.z * sl, v3 = xv.w * sl;
+  const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1, h2 = (_Float16)v2, h3 = (_Float16)v3;
+  // lo is stored times 2^11 (exact: a power of two), so that its products
+  // stay as large as hi's inside the matrix cores' sums.
+  const _Float16 l0 = (_Float16)((v0 - (float)h0) * 2048.f), l1 = (_Float16)((v1 - (float)h1) * 2048.f);
+  const _Float16 l2 = (_Float16)((v2 - (float)h2) * 2048.f), l3 = (_Float16)((v3 - (float)h3) * 2048.f);
+  float su = (xv.x + xv.y) + (xv.z + xv.w);
+  su += dpp_from<0xB1>(su, 0.f);
+  su += dpp_from<0x4E>(su, 0.f);
+  if (KIND == Q4_K) su += dpp_from<0x114>(su, 0.f);  // 32-element sub-blocks: two quads
+  *reinterpret_cast<uint2*>(L.wr_hi) = make_uint2(pack_f16x2(h0, h2), pack_f16x2(h1, h3));
+  *reinterpret_cast<uint2*>(L.wr_hi + 4) = make_uint2(pack_f16x2(l0, l2), pack_f16x2(l1, l3));
+  if (L.xs_writer) xsum[L.xs_pos] = su * S;
+  return ldexpf(1.f, -se);
+}
+
+// One super-block column of RB 16-row blocks (RB = 4: the whole 64-row tile;
+// RB = 1: block rb0 of it) as lane (n, g) loads it.
+template <int KIND, int RB> struct MvCol;
+
+// Q4_K: the header (d, dmin, scales) -- with RB = 4 of row `lane`, one
+// coalesced 1 KB load shared through LDS; with RB = 1 of the lane's own row
+// 16 rb0 + n -- and the qs chunks 1 + 2g, 2 + 2g of rows 16 rb + n.
+template <int RB> struct MvCol<Q4_K, RB> {
+  uint4 h, a[RB], b[RB];
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
+    const int n = lane & 15, g = lane >> 4;
+    h = ld16(grp + (RB == 4 ? lane : 16 * rb0 + n) * 16);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
+      a[rb] = ld16(r + (1 + 2 * g) * 1024);
+      b[rb] = ld16(r + (2 + 2 * g) * 1024);
+    }
+  }
+};
+
+// Q6_K (g = 2h + t): ql chunks 4h + t (codes k = 0, 2), 4h + 2 + t (k = 1, 3)
+// and qh chunk 8 + 2h + t of rows 16 rb + n; the scale chunk 12 and d of row
+// `lane` (RB = 4) or of the lane's own row (RB = 1).
+template <int RB> struct MvCol<Q6_K, RB> {
+  uint4 a[RB], b[RB], q[RB], sc;
+  uint32_t d;
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
+    const int n = lane & 15, g = lane >> 4, h = g >> 1, t = g & 1;
+    const int hr = RB == 4 ? lane : 16 * rb0 + n;
+    sc = ld16(grp + 12 * 1024 + hr * 16);
+    d = ld2(grp + 13 * 1024 + hr * 2);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
+      a[rb] = ld16(r + (4 * h + t) * 1024);
+      b[rb] = ld16(r + (4 * h + 2 + t) * 1024);
+      q[rb] = ld16(r + (8 + 2 * h + t) * 1024);
+    }
+  }
+};
+
+// Bytes 0 and 2 of z as two f16 halves, and bytes 1 and 3.
+__device__ __forceinline__ uint32_t bytes02(uint32_t z) { return __builtin_amdgcn_perm(z, z, 0x0C020C00u); }
+__device__ __forceinline__ uint32_t bytes13(uint32_t z) { return __builtin_amdgcn_perm(z, z, 0x0C030C01u); }
+
+// The per-row header words of a column, shared through LDS.
+template <int KIND> struct MvHdr;
+template <> struct MvHdr<Q4_K> {
+  uint4 h[64];
+};
+template <> struct MvHdr<Q6_K> {
+  uint4 sc[64];
+  uint32_t d[64];
+};
+
+// Lane `lane`'s A fragment of MFMA j: from the full image, or from the
+// compact one (the 16 data lanes 20 grp + r, r < 4, read their slot, the
+// others the zero slot).
+template <int IL>
+__device__ __forceinline__ uint4 img_frag(const uint4 (&img)[8][IL], int j, int lane) {
+  if (IL == 64) return img[j][lane];
+  const int grp = lane >> 4, m = lane & 15;
+  return img[j][(m >> 2) == grp ? 4 * grp + (m & 3) : 16];
+}
+
+__device__ __forceinline__ uint32_t dword_of(const uint4& v, int j) {
+  return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+
+// One super-block column of RB row blocks: the A image, the row blocks' MFMA
+// chains interleaved (consecutive MFMAs independent), then the scales.
+template <int RB>
+__device__ __forceinline__ void mv_column(const MvCol<Q4_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q4_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  const int g = lane >> 4, n = lane & 15;
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q4_K>(xv, L, xsum);
+  if (RB == 4) hdr->h[lane] = c.h;
+  __builtin_amdgcn_wave_barrier();
+  uint4 A[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) A[j] = img_frag(img, j, lane);
+  const float2 X = *reinterpret_cast<const float2*>(&xsum[2 * g]);
+  uint4 H[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) H[rb] = RB == 4 ? hdr->h[16 * rb + n] : c.h;
+  __builtin_amdgcn_wave_barrier();
+  mf4 D[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) D[rb] = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint32_t q = dword_of(j < 4 ? c.a[rb] : c.b[rb], j & 3);
+      const uint32_t t = q >> 8;
+      D[rb] = mfma_f16(A[j], make_uint4(q & 0x000F000Fu, t & 0x000F000Fu, q & 0x00F000F0u, t & 0x00F000F0u), D[rb]);
+    }
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const uint4 h = H[rb];
+    const float sa = __builtin_fmaf(D[rb][1], 1.f / 2048.f, D[rb][0]);
+    const float sb = __builtin_fmaf(D[rb][3], 1.f / 2048.f, D[rb][2]);
+    const uint32_t psc = L.upper ? h.w : h.y, pm = L.upper ? h.w : h.z;
+    const uint32_t scp = ((psc >> L.b0) & L.m1) | ((h.y >> (L.b0 + 2u)) & L.m2);
+    const uint32_t mp = ((pm >> L.mshift) & L.m1) | ((h.z >> (L.b0 + 2u)) & L.m2);
+    const float sca = (float)(scp & 0xFFu), scb = (float)((scp >> 8) & 0xFFu);
+    const float ma = (float)(mp & 0xFFu), mb = (float)((mp >> 8) & 0xFFu);
+    const float T = __builtin_fmaf(scb, sb, sca * sa);
+    const float M = __builtin_fmaf(mb, X.y, ma * X.x);
+    const float d = f16_ada(h.x & 0xFFFFu) * 16777216.f, dmin = f16_ada(h.x >> 16);
+    acc[rb] = __builtin_fmaf(__builtin_fmaf(d, T, -(dmin * M)), invS, acc[rb]);
+  }
+}
+
+template <int RB>
+__device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q6_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  const int g = lane >> 4, n = lane & 15;
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q6_K>(xv, L, xsum);
+  if (RB == 4) {
+    hdr->sc[lane] = c.sc;
+    hdr->d[lane] = c.d;
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint4 A[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) A[j] = img_frag(img, j, lane);
+  const float4 X = *reinterpret_cast<const float4*>(&xsum[4 * g]);  // sub-blocks k = 0..3 of quarter g
+  uint2 SC[RB];
+  uint32_t DD[RB];
+  const bool half1 = g >= 2;  // the scales of half 1 are dwords 2, 3 of the scale chunk
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const uint4 s4 = RB == 4 ? hdr->sc[16 * rb + n] : c.sc;
+    SC[rb] = half1 ? make_uint2(s4.z, s4.w) : make_uint2(s4.x, s4.y);
+    DD[rb] = RB == 4 ? hdr->d[16 * rb + n] : c.d;
+  }
+  __builtin_amdgcn_wave_barrier();
+  mf4 D0[RB], D1[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) D0[rb] = D1[rb] = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint32_t a = dword_of(c.a[rb], j), b = dword_of(c.b[rb], j), q = dword_of(c.q[rb], j);
+      // 6-bit codes of sub-blocks k = 0..3 as bytes (as Block<Q6_K>::dot).
+      const uint32_t z0 = (a & 0x0F0F0F0Fu) | ((q << 4) & 0x30303030u);
+      const uint32_t z1 = (b & 0x0F0F0F0Fu) | ((q << 2) & 0x30303030u);
+      const uint32_t z2 = ((a >> 4) & 0x0F0F0F0Fu) | (q & 0x30303030u);
+      const uint32_t z3 = ((b >> 4) & 0x0F0F0F0Fu) | ((q >> 2) & 0x30303030u);
+      D0[rb] = mfma_f16(A[j], make_uint4(bytes02(z0), bytes13(z0), bytes02(z1), bytes13(z1)), D0[rb]);
+      D1[rb] = mfma_f16(A[4 + j], make_uint4(bytes02(z2), bytes13(z2), bytes02(z3), bytes13(z3)), D1[rb]);
+    }
+  }
+  const int tb = 8 * (g & 1);  // byte t of each scale dword
+  constexpr float K32 = 32.f / 16777216.f;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const float s0 = __builtin_fmaf(D0[rb][1], 1.f / 2048.f, D0[rb][0]);
+    const float s1 = __builtin_fmaf(D0[rb][3], 1.f / 2048.f, D0[rb][2]);
+    const float s2 = __builtin_fmaf(D1[rb][1], 1.f / 2048.f, D1[rb][0]);
+    const float s3 = __builtin_fmaf(D1[rb][3], 1.f / 2048.f, D1[rb][2]);
+    // int8 scales sc[8h + t + 2k]: dword 2h holds k = 0, 1; dword 2h + 1 holds k = 2, 3.
+    const float c0 = (float)(int32_t)__builtin_amdgcn_sbfe(SC[rb].x, tb, 8);
+    const float c1 = (float)(int32_t)__builtin_amdgcn_sbfe(SC[rb].x, tb + 16, 8);
+    const float c2 = (float)(int32_t)__builtin_amdgcn_sbfe(SC[rb].y, tb, 8);
+    const float c3 = (float)(int32_t)__builtin_amdgcn_sbfe(SC[rb].y, tb + 16, 8);
+    // The codes are stored offset by 32: sum (q - 32) x = sum q x - 32 sum x.
+    float T = c0 * __builtin_fmaf(-K32, X.x, s0);
+    T = __builtin_fmaf(c1, __builtin_fmaf(-K32, X.y, s1), T);
+    T = __builtin_fmaf(c2, __builtin_fmaf(-K32, X.z, s2), T);
+    T = __builtin_fmaf(c3, __builtin_fmaf(-K32, X.w, s3), T);
+    const float d = f16_ada(DD[rb]) * 16777216.f;
+    acc[rb] = __builtin_fmaf(d * T, invS, acc[rb]);
+  }
+}
+
+// The LDS one wave uses: its A image, sub-block sums and row headers.
+template <int KA, int KB>
+struct MvShared {
+  uint4 img[8][64];
+  float xsum[16];
+  union {
+    MvHdr<KA> a;
+    MvHdr<KB> b;
+  } hdr;
+};
+
+// The LDS one wave of the 16-row kernels uses: the compact A image and the
+// sub-block sums (headers come straight from the lane's own row).
+struct MvShared16 {
+  uint4 img[8][17];
+  float xsum[16];
+};
+
+// Row `lane` of tile `tile`'s partial dot over super-block columns sb0 ..
+// sb0 + spw - 1 of packed matrix P (nsb columns), computed by this wave.
+// How a wave walks its columns: one column; two register sets in turn (the
+// next column's loads in flight during this one's work); one register set,
+// columns one after another (fewer registers, so more waves per CU).
+constexpr int MV_ONE = 0, MV_PF = 1, MV_SEQ = 2;
+
+//
+// RB = 4: the wave covers the whole 64-row tile and lane l returns row l.
+// RB = 1: it covers 16-row block rb0 of the tile and lane l returns row
+// 16 rb0 + l % 16.
+template <int KIND, int PIPE, int RB = 4>
+__device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int nsb, int tile, int sb0, int spw,
+                                              const float* __restrict__ x, uint4 (&img)[8][RB == 4 ? 64 : 17],
+                                              float* xsum, MvHdr<KIND>* hdr, int lane, int rb0 = 0) {
+  constexpr int GB = 64 * Block<KIND>::BYTES;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (RB == 4 || lane < 17) img[j][lane] = make_uint4(0u, 0u, 0u, 0u);
+  const MvLane L = mv_lane<KIND>(img, lane);
+
+  float acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.f;
+  const uint8_t* gp = P + ((size_t)tile * nsb + sb0) * GB;
+  const float* xp = x + (size_t)sb0 * 256 + 4 * lane;
+
+  MvCol<KIND, RB> c0;
+  float4 x0;
+  c0.load(gp, lane, rb0);
+  __builtin_memcpy(&x0, __builtin_assume_aligned(xp, 16), 16);
+  if (PIPE == MV_ONE) {
+    mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+  } else if (PIPE == MV_SEQ) {  // columns one after another: one register set, more waves per CU
+    for (int s = 0; s < spw; ++s) {
+      if (s > 0) {
+        asm volatile("" ::: "memory");  // the next column's loads stay after this column's work
+        c0.load(gp + (size_t)s * GB, lane, rb0);
+        __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)s * 256, 16), 16);
+      }
+      mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+    }
+  } else {
+    // Two register sets used in turn: the next column's loads are in flight
+    // while the current one is multiplied, with no copies between them.
+    MvCol<KIND, RB> c1;
+    float4 x1;
+    for (int s = 0; s < spw; s += 2) {
+      const int s1 = s + 1 < spw ? s + 1 : s;
+      c1.load(gp + (size_t)s1 * GB, lane, rb0);
+      __builtin_memcpy(&x1, __builtin_assume_aligned(xp + (size_t)s1 * 256, 16), 16);
+      asm volatile("" ::: "memory");  // keep these loads issued here
+      mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+      if (s + 2 < spw) {
+        c0.load(gp + (size_t)(s + 2) * GB, lane, rb0);
+        __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)(s + 2) * 256, 16), 16);
+        asm volatile("" ::: "memory");
+      }
+      if (s + 1 < spw) mv_column(c1, x1, L, img, xsum, hdr, lane, acc);
+    }
+  }
+
+  // Lane (n, g) holds rows 16 rb + n over its quarter: add the four quarters
+  // (ascending g).
+  float* red = reinterpret_cast<float*>(&img[0][0]);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) red[rb * 64 + lane] = acc[rb];
+  __builtin_amdgcn_wave_barrier();
+  const float* rr = red + (RB == 4 ? (lane >> 4) * 64 : 0) + (lane & 15);
+  return ((rr[0] + rr[16]) + rr[32]) + rr[48];
+}
+
+}  // namespace kq

@@ -106,8 +106,8 @@ def test_grouped_moe_rejects_bad_arguments(lib):
     pointers are never dereferenced)."""
     assert lib.aspida_moe_packed_work_bytes(0, 2048, 768, 8) < 0
     assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 33) < 0
-    # one token: h 9 x 768, yk 9 x 2048 floats, gsh, 32 tile counters of 256 B
-    assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 8) == 4 * 9 * (768 + 2048) + 256 + 32 * 256
+    # one token: h 9 x 768, yk 9 x 2048 floats, gsh, 128 counters (16-row blocks of dim) of 256 B
+    assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 8) == 4 * 9 * (768 + 2048) + 256 + 128 * 256
     # T * top_k above the per-launch job bound: sized for one chunk of 128 tokens
     assert lib.aspida_moe_packed_work_bytes(1000, 2048, 768, 8) == lib.aspida_moe_packed_work_bytes(128, 2048, 768, 8)
     one = 256
