@@ -193,7 +193,8 @@ struct MvWorkspace {
 // 16-vector kernel; beyond 16 the 16-vector kernel in launches of 16 when
 // the matrix has at least MM16_MIN_UNITS (64-row tile, super-block column)
 // pairs to spread, else the 64-vector kernel, which then takes the batch in
-// fewer launches.  Q6_K: VALU up to 4, then the 64-vector kernel.
+// fewer launches.  Q6_K: VALU up to 4, then the 64-vector kernel in launches
+// of up to 32.
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;
@@ -209,7 +210,10 @@ hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int b
                                   (batch <= 16 || units >= MM16_MIN_UNITS)));
   const bool mm64 = !mm16 && kq::mfma_kind(kind) && (eng == 2 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS));
   if (mm16 || mm64) {
-    const int step = mm16 ? 16 : 64;
+    // Q6_K in launches of at most 32 vectors: the 64-vector kernel's Q6_K
+    // variant runs out of registers above 32 (14336x4096: 359 us for 64
+    // vectors in one launch, 82 us per 32).
+    const int step = mm16 ? 16 : kind == kq::Q6_K ? 32 : 64;
     for (int b0 = 0; b0 < batch; b0 += step) {
       const int nb = std::min(step, batch - b0);
       const float* xb = X + (size_t)b0 * in_dim;

@@ -523,7 +523,8 @@ static hipError_t launch_down1_kind(const MoeGroupedArgs& a, hipStream_t s) {
 
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s) {
   // One token with matrix-core kinds throughout: the one-token kernels.
-  if (a.T == 1 && matvec_mfma_takes(gu_kind) && matvec_mfma_takes(down_kind) &&
+  const auto mfma_moe = [](int k) { return (k == Q4_K || k == Q6_K) && matvec_mfma_takes(k); };
+  if (a.T == 1 && mfma_moe(gu_kind) && mfma_moe(down_kind) &&
       (a.top_k + 1) * (a.I / 256) <= MOE1_MAX_UNITS) {
     const hipError_t e = gu_kind == Q4_K ? launch_gate_up1_kind<Q4_K>(a, s) : launch_gate_up1_kind<Q6_K>(a, s);
     if (e != hipSuccess) return e;

@@ -146,6 +146,22 @@ template <int RB> struct MvCol<Q6_K, RB> {
   }
 };
 
+// Q2_K (quarter c = 2 nh + g): qs chunk 1 + c (fields k = 0..3 of elements
+// l = 0..15) of rows 16 rb + n; the scale chunk 0 and d | dmin << 16 of row
+// `lane` (RB = 4) or of the lane's own row (RB = 1).
+template <int RB> struct MvCol<Q2_K, RB> {
+  uint4 q[RB], sc;
+  uint32_t d;
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
+    const int n = lane & 15, c = lane >> 4;
+    const int hr = RB == 4 ? lane : 16 * rb0 + n;
+    sc = ld16(grp + hr * 16);
+    d = ld4(grp + 5 * 1024 + hr * 4);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) q[rb] = ld16(grp + (1 + c) * 1024 + (16 * (rb0 + rb) + n) * 16);
+  }
+};
+
 // Bytes 0 and 2 of z as two f16 halves, and bytes 1 and 3.
 __device__ __forceinline__ uint32_t bytes02(uint32_t z) { return __builtin_amdgcn_perm(z, z, 0x0C020C00u); }
 __device__ __forceinline__ uint32_t bytes13(uint32_t z) { return __builtin_amdgcn_perm(z, z, 0x0C030C01u); }
@@ -156,6 +172,10 @@ template <> struct MvHdr<Q4_K> {
   uint4 h[64];
 };
 template <> struct MvHdr<Q6_K> {
+  uint4 sc[64];
+  uint32_t d[64];
+};
+template <> struct MvHdr<Q2_K> {
   uint4 sc[64];
   uint32_t d[64];
 };
@@ -285,6 +305,74 @@ __device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, c
     T = __builtin_fmaf(c3, __builtin_fmaf(-K32, X.w, s3), T);
     const float d = f16_ada(DD[rb]) * 16777216.f;
     acc[rb] = __builtin_fmaf(d * T, invS, acc[rb]);
+  }
+}
+
+// Q2_K: element 128 nh + 32 k + 16 g + l is field k of qs byte
+// 32 nh + 16 g + l with scale/min byte 8 nh + 2 k + g (Decode_Q2K_Block,
+// llm_dequant.adb:304-320) -- the element and sub-block layout of Q6_K's
+// quarters, so the A image is Q6_K's.  MFMA (T, j) takes fields 2T, 2T + 1 of
+// qs dword j left in place: code q of field k is the subnormal q 2^(2k-24),
+// whose factor 4^k the scales absorb.
+template <int RB>
+__device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q2_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  const int g = lane >> 4, n = lane & 15;
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q2_K>(xv, L, xsum);
+  if (RB == 4) {
+    hdr->sc[lane] = c.sc;
+    hdr->d[lane] = c.d;
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint4 A[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) A[j] = img_frag(img, j, lane);
+  const float4 X = *reinterpret_cast<const float4*>(&xsum[4 * g]);  // sub-blocks k = 0..3 of quarter g
+  uint2 SC[RB];
+  uint32_t DD[RB];
+  const bool nh1 = g >= 2;  // scale bytes 8 nh + 2k + g: dwords 2 nh (k < 2) and 2 nh + 1
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const uint4 s4 = RB == 4 ? hdr->sc[16 * rb + n] : c.sc;
+    SC[rb] = nh1 ? make_uint2(s4.z, s4.w) : make_uint2(s4.x, s4.y);
+    DD[rb] = RB == 4 ? hdr->d[16 * rb + n] : c.d;
+  }
+  __builtin_amdgcn_wave_barrier();
+  mf4 D0[RB], D1[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) D0[rb] = D1[rb] = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint32_t w = dword_of(c.q[rb], j), t = w >> 8;
+      D0[rb] = mfma_f16(A[j], make_uint4(w & 0x00030003u, t & 0x00030003u, w & 0x000C000Cu, t & 0x000C000Cu), D0[rb]);
+      D1[rb] = mfma_f16(A[4 + j], make_uint4(w & 0x00300030u, t & 0x00300030u, w & 0x00C000C0u, t & 0x00C000C0u),
+                        D1[rb]);
+    }
+  }
+  const uint32_t tb = 8u * (uint32_t)(g & 1);  // byte 2 (k % 2) + g of each scale dword
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const float s0 = __builtin_fmaf(D0[rb][1], 1.f / 2048.f, D0[rb][0]);
+    const float s1 = __builtin_fmaf(D0[rb][3], 1.f / 2048.f, D0[rb][2]);
+    const float s2 = __builtin_fmaf(D1[rb][1], 1.f / 2048.f, D1[rb][0]);
+    const float s3 = __builtin_fmaf(D1[rb][3], 1.f / 2048.f, D1[rb][2]);
+    const uint32_t b0 = bfe(SC[rb].x, tb, 8), b1 = bfe(SC[rb].x, tb + 16, 8);
+    const uint32_t b2 = bfe(SC[rb].y, tb, 8), b3 = bfe(SC[rb].y, tb + 16, 8);
+    // scale = low nibble, min = high nibble (llm_dequant.adb:304-320).
+    float T = (float)(b0 & 15u) * s0;
+    T = __builtin_fmaf((float)(b1 & 15u) * 0.25f, s1, T);
+    T = __builtin_fmaf((float)(b2 & 15u) * 0.0625f, s2, T);
+    T = __builtin_fmaf((float)(b3 & 15u) * 0.015625f, s3, T);
+    float M = (float)(b0 >> 4) * X.x;
+    M = __builtin_fmaf((float)(b1 >> 4), X.y, M);
+    M = __builtin_fmaf((float)(b2 >> 4), X.z, M);
+    M = __builtin_fmaf((float)(b3 >> 4), X.w, M);
+    const float d = f16_ada(DD[rb] & 0xFFFFu) * 16777216.f, dmin = f16_ada(DD[rb] >> 16);
+    acc[rb] = __builtin_fmaf(__builtin_fmaf(d, T, -(dmin * M)), invS, acc[rb]);
   }
 }
 

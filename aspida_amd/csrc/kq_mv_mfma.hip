@@ -154,7 +154,7 @@ static std::atomic<int> g_engine{0};
 
 void set_matvec_engine(int engine) { g_engine = engine; }
 
-bool matvec_mfma_takes(int kind) { return (kind == Q4_K || kind == Q6_K) && g_engine.load() == 0; }
+bool matvec_mfma_takes(int kind) { return (kind == Q4_K || kind == Q6_K || kind == Q2_K) && g_engine.load() == 0; }
 
 // The kernel a plan runs: NW waves per workgroup and the column walk.
 static int mv_pipe(const PackedPlan& p) { return p.spw == 1 ? MV_ONE : p.seq ? MV_SEQ : MV_PF; }
@@ -270,7 +270,11 @@ static hipError_t launch_mfma_kind(const uint8_t* w, int in_dim, int out_dim, co
   return hipGetLastError();
 }
 
-bool matvec2_mfma_takes(int kind_a, int kind_b) { return matvec_mfma_takes(kind_a) && matvec_mfma_takes(kind_b); }
+// The pair kernels are built for Q4_K and Q6_K.
+bool matvec2_mfma_takes(int kind_a, int kind_b) {
+  return (kind_a == Q4_K || kind_a == Q6_K) && (kind_b == Q4_K || kind_b == Q6_K) && matvec_mfma_takes(kind_a) &&
+         matvec_mfma_takes(kind_b);
+}
 
 template <int KA, int KB>
 static hipError_t launch_mfma_pair(const uint8_t* a, int out_a, float* ya, const uint8_t* b, int out_b, float* yb,
@@ -343,6 +347,7 @@ hipError_t launch_matvec_mfma(int kind, const void* P, int in_dim, int out_dim, 
   switch (kind) {
     case Q4_K: return launch_mfma_kind<Q4_K>(w, in_dim, out_dim, x, y, part, count, s);
     case Q6_K: return launch_mfma_kind<Q6_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q2_K: return launch_mfma_kind<Q2_K>(w, in_dim, out_dim, x, y, part, count, s);
     default: return hipErrorNotSupported;
   }
 }

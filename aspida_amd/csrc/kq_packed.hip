@@ -280,8 +280,10 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   // every CU (otherwise few CUs would walk long column runs).  Measured on
   // MI355X: Q4_K 4096x4096 4.3 us against 5.8 us on 64-row workgroups with
   // partial sums; 1024x14336 5.9 us on 64-row workgroups against 8.1 us.
+  // Q2_K streams fewer bytes per column for the same arithmetic, so long
+  // column runs stay on 64-row workgroups (4096x14336: 8.6 us against 9.1).
   const int nsb = in_dim / 256;
-  if (4L * ntiles <= 2L * cus && (nsb <= 16 || 4L * ntiles >= cus)) return mfma16_plan(nsb);
+  if (4L * ntiles <= 2L * cus && (nsb <= 16 || (4L * ntiles >= cus && kind != Q2_K))) return mfma16_plan(nsb);
   return mfma64_plan(kind, in_dim, out_dim);
 }
 
@@ -314,7 +316,7 @@ static PackedPlan mfma64_plan(int kind, int in_dim, int out_dim) {
 
 size_t packed_workspace_floats(int in_dim, int out_dim) {
   const int ks = std::max({packed_plan(in_dim, out_dim).ks, mfma_plan(Q4_K, in_dim, out_dim).ks,
-                           mfma_plan(Q6_K, in_dim, out_dim).ks});
+                           mfma_plan(Q6_K, in_dim, out_dim).ks, mfma_plan(Q2_K, in_dim, out_dim).ks});
   return ks > 1 ? (size_t)ks * ((out_dim + 63) / 64) * 64 : 0;
 }
 

@@ -323,7 +323,7 @@ def small_batch_table(torch, aa, synth, seed, stream):
                 t = e0.elapsed_time(e1) * 1e-3 / (3 * ncopy)
                 nbytes = aa.weight_bytes(kind, inp, out) + 4 * B * (inp + out)
                 table[f"{aa.KIND_NAMES[kind]} {out}x{inp} B={B}"] = {
-                    "kernel": "kq_mm_packed_valu" if B <= 4 else "kq_mm_mfma",
+                    "kernel": small_batch_kernel(aa, kind, inp, out, B),
                     "us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
                     "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3),
                     "TFLOPs": round(2.0 * B * inp * out / t / 1e12, 2)}
@@ -333,6 +333,18 @@ def small_batch_table(torch, aa, synth, seed, stream):
             del P
             torch.cuda.empty_cache()
     return table
+
+
+def small_batch_kernel(aa, kind, inp, out, B):
+    """The kernel the library's default small-batch pick runs (matmul_packed in
+    aspidagpu.hip): the multi-vector VALU kernel up to 4 vectors; Q4_K then the
+    16-vector MFMA kernel (above 16 vectors only for matrices of >= 2048
+    64-row-by-256-column blocks), else the 64-vector MFMA kernel."""
+    if B <= 4:
+        return "kq_mm_packed_valu"
+    if kind == aa.Q4_K and (B <= 16 or (-(-out // 64)) * (inp // 256) >= 2048):
+        return "kq_mm16_q4k"
+    return "kq_mm_mfma"
 
 
 def moe_table(torch, aa, synth, seed, stream):

@@ -352,7 +352,7 @@ def _x_variants(in_dim, gen):
 
 
 @pytest.mark.parametrize("engine", [0, 1], ids=["mfma", "valu"])
-@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K, aa.Q2_K], ids=["Q4_K", "Q6_K", "Q2_K"])
 def test_engines_activation_range(kind, engine, dev):
     """Both batch-1 engines for Q4_K and Q6_K against the oracle, over
     activations whose magnitudes span the f32 range, at shapes that take every
@@ -376,7 +376,11 @@ def test_engines_activation_range(kind, engine, dev):
                 dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
                 sync()
                 want = oracle.qmatvec(kind, w, in_dim, out_dim, x, nthreads=ncpu())
-                rtol = MFMA_RTOL if engine == 0 and name in ("outliers", "mixed") else MV_RTOL
+                # Q2_K's 2-bit codes with mins: for an outlier element d sc q and dmin m nearly
+                # cancel, so the matrix cores' error relative to the large q x term weighs more
+                # against sum |w x| (measured 1.3e-4; the north-star bar is 1e-3).
+                rtol = (MFMA_RTOL * (3 if kind == aa.Q2_K else 1) if engine == 0 and name in ("outliers", "mixed")
+                        else MV_RTOL)
                 r = assert_close_scaled(dy.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x),
                                         rtol=rtol, what=f"engine {engine} {out_dim}x{in_dim} {name}")
                 print(f"  max err / sum|wx| = {r:.2e}", flush=True)
@@ -394,7 +398,7 @@ MFMA_SHAPE_CASES = [(64, 4096), (130, 4096), (1000, 2048), (4096, 4096), (300, 1
 
 @pytest.mark.parametrize("pipe", [0, 1, 2], ids=["plan", "prefetch", "sequential"])
 @pytest.mark.parametrize("rows", [1, 2], ids=["rows64", "rows16"])
-@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K, aa.Q2_K], ids=["Q4_K", "Q6_K", "Q2_K"])
 def test_mfma_workgroup_shapes(kind, rows, pipe, dev):
     dev.set_mfma_rows(rows)
     dev.lib.aspida_kq_set_mfma_pipeline(pipe)
