@@ -225,10 +225,10 @@ void set_mfma_rows(int mode) { g_mfma_rows = mode; }
 // 16-row workgroups (kq_mv_mfma16): as many waves as divide the columns, up
 // to 16 (the instantiated counts), several columns per wave taken one after
 // another (measured faster than prefetching on MI355X).
-static PackedPlan mfma16_plan(int nsb) {
+static PackedPlan mfma16_plan(int nsb, int max_nw = 16) {
   PackedPlan p{1, 1, nsb};
   for (int n : {16, 14, 8, 4, 2, 1})
-    if (nsb % n == 0) {
+    if (n <= max_nw && nsb % n == 0) {
       p.nw = n;
       break;
     }
@@ -246,7 +246,7 @@ PackedPlan mfma_plan(int kind, int in_dim, int out_dim) {
   const int pipe = g_mfma_pipe, rows = g_mfma_rows;
   PackedPlan p = mfma_plan_choice(kind, in_dim, out_dim);
   if (rows == 2 || (rows == 0 && p.blk16)) {
-    p = mfma16_plan(nsb);
+    if (!p.blk16) p = mfma16_plan(nsb);
     const int onw = g_plan_nw;
     if ((onw == 16 || onw == 14 || onw == 8 || onw == 4 || onw == 2 || onw == 1) && nsb % onw == 0) {
       p.nw = onw;
@@ -284,6 +284,9 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   // column runs stay on 64-row workgroups (4096x14336: 8.6 us against 9.1).
   const int nsb = in_dim / 256;
   if (4L * ntiles <= 2L * cus && (nsb <= 16 || (4L * ntiles >= cus && kind != Q2_K))) return mfma16_plan(nsb);
+  // Very tall Q6_K matrices (the output head): 16-row workgroups of 8 waves
+  // walking 2+ columns each (128256x4096: 71.5 us against 77.3 on 64-row).
+  if (kind == Q6_K && ntiles >= 4L * cus) return mfma16_plan(nsb, 8);
   return mfma64_plan(kind, in_dim, out_dim);
 }
 

@@ -421,3 +421,13 @@ def test_packed_matvec_pair_workgroup_shapes(case, rows, dev):
         test_packed_matvec_pair(case, dev)
     finally:
         dev.set_mfma_rows(0)
+
+
+def test_tall_q6k_head_plan(dev):
+    """A Q6_K matrix of more than 1024 64-row tiles (the output head's shape
+    class) takes 16-row workgroups of 8 waves, 2 columns each, and matches
+    the oracle."""
+    kind, out_dim, in_dim = aa.Q6_K, 65600, 4096
+    plan = dev.matvec_plan(kind, in_dim, out_dim)
+    assert plan[0] and plan[5] and plan[1] == 8 and plan[3] == 2, plan
+    _check_dev(dev, kind, out_dim, in_dim, 6161, "packed", f"Q6_K {out_dim}x{in_dim} plan={plan}")
