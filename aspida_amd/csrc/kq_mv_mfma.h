@@ -53,7 +53,7 @@ __device__ __forceinline__ MvLane mv_lane(uint4 (&img)[8][IL], int lane) {
   L.m1 = L.upper ? 0x0F0Fu : 0x3F3Fu;
   L.m2 = L.upper ? 0x3030u : 0u;
   L.mshift = L.b0 + (L.upper ? 4u : 0u);
-  if (KIND == Q4_K) {
+  if (KIND == Q4_K || KIND == Q5_K) {
     // Elements 4 lane .. +3 = elements 4 bj .. of sub-block bs: MFMA bj, rows
     // m = 2 bs (+1) of k-group bs / 2, dwords 2 (bs % 2) + {0, 1}.
     const int bs = lane >> 3, bj = lane & 7;
@@ -97,7 +97,7 @@ __device__ __forceinline__ float build_image(float4 xv, const MvLane& L, float* 
   float su = (xv.x + xv.y) + (xv.z + xv.w);
   su += dpp_from<0xB1>(su, 0.f);
   su += dpp_from<0x4E>(su, 0.f);
-  if (KIND == Q4_K) su += dpp_from<0x114>(su, 0.f);  // 32-element sub-blocks: two quads
+  if (KIND == Q4_K || KIND == Q5_K) su += dpp_from<0x114>(su, 0.f);  // 32-element sub-blocks: two quads
   *reinterpret_cast<uint2*>(L.wr_hi) = make_uint2(pack_f16x2(h0, h2), pack_f16x2(h1, h3));
   *reinterpret_cast<uint2*>(L.wr_hi + 4) = make_uint2(pack_f16x2(l0, l2), pack_f16x2(l1, l3));
   if (L.xs_writer) xsum[L.xs_pos] = su * S;
@@ -146,6 +146,26 @@ template <int RB> struct MvCol<Q6_K, RB> {
   }
 };
 
+// Q5_K: as Q4_K (header chunk 0; quarter g's qs chunks 3 + 2g, 4 + 2g), plus
+// the qh chunks 1 and 2 of rows 16 rb + n (the fifth bits of elements
+// l = 0..15 and 16..31 of every quarter; bit 2g for sub-block 2g, 2g + 1 for
+// 2g + 1).
+template <int RB> struct MvCol<Q5_K, RB> {
+  uint4 h, a[RB], b[RB], ha[RB], hb[RB];
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
+    const int n = lane & 15, g = lane >> 4;
+    h = ld16(grp + (RB == 4 ? lane : 16 * rb0 + n) * 16);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
+      a[rb] = ld16(r + (3 + 2 * g) * 1024);
+      b[rb] = ld16(r + (4 + 2 * g) * 1024);
+      ha[rb] = ld16(r + 1 * 1024);
+      hb[rb] = ld16(r + 2 * 1024);
+    }
+  }
+};
+
 // Q2_K (quarter c = 2 nh + g): qs chunk 1 + c (fields k = 0..3 of elements
 // l = 0..15) of rows 16 rb + n; the scale chunk 0 and d | dmin << 16 of row
 // `lane` (RB = 4) or of the lane's own row (RB = 1).
@@ -169,6 +189,9 @@ __device__ __forceinline__ uint32_t bytes13(uint32_t z) { return __builtin_amdgc
 // The per-row header words of a column, shared through LDS.
 template <int KIND> struct MvHdr;
 template <> struct MvHdr<Q4_K> {
+  uint4 h[64];
+};
+template <> struct MvHdr<Q5_K> {
   uint4 h[64];
 };
 template <> struct MvHdr<Q6_K> {
@@ -305,6 +328,64 @@ __device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, c
     T = __builtin_fmaf(c3, __builtin_fmaf(-K32, X.w, s3), T);
     const float d = f16_ada(DD[rb]) * 16777216.f;
     acc[rb] = __builtin_fmaf(d * T, invS, acc[rb]);
+  }
+}
+
+// Q5_K (Decode_Q5K_Block, llm_dequant.adb:426-498): Q4_K's columns with a
+// fifth code bit, code = nibble + 16 hbit.  The nibbles take Q4_K's MFMAs; the
+// fifth bits take one more MFMA each, against the same activation fragments,
+// with qh dword j's bit 2g (sub-block 2g) and 2g + 1 (sub-block 2g + 1) left
+// in place as the subnormals 2^(2g-24) and 2^(2g+1-24).  Their sums are
+// scaled back per lane: 16 2^-2g for sub-block 2g, and 16 2^-(2g+1) 16 for
+// 2g + 1, whose activations the image holds divided by 16.
+template <int RB>
+__device__ __forceinline__ void mv_column(const MvCol<Q5_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q5_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  const int g = lane >> 4, n = lane & 15;
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q5_K>(xv, L, xsum);
+  if (RB == 4) hdr->h[lane] = c.h;
+  __builtin_amdgcn_wave_barrier();
+  uint4 A[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) A[j] = img_frag(img, j, lane);
+  const float2 X = *reinterpret_cast<const float2*>(&xsum[2 * g]);
+  uint4 H[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) H[rb] = RB == 4 ? hdr->h[16 * rb + n] : c.h;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t m0 = 0x00010001u << (2 * g), m1 = 0x00020002u << (2 * g);
+  mf4 D[RB], E[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) D[rb] = E[rb] = mf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint32_t q = dword_of(j < 4 ? c.a[rb] : c.b[rb], j & 3), t = q >> 8;
+      const uint32_t hq = dword_of(j < 4 ? c.ha[rb] : c.hb[rb], j & 3), ht = hq >> 8;
+      D[rb] = mfma_f16(A[j], make_uint4(q & 0x000F000Fu, t & 0x000F000Fu, q & 0x00F000F0u, t & 0x00F000F0u), D[rb]);
+      E[rb] = mfma_f16(A[j], make_uint4(hq & m0, ht & m0, hq & m1, ht & m1), E[rb]);
+    }
+  }
+  const float fa = 16.f * __builtin_ldexpf(1.f, -2 * g), fb = 128.f * __builtin_ldexpf(1.f, -2 * g);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const uint4 h = H[rb];
+    const float ea = __builtin_fmaf(E[rb][1], 1.f / 2048.f, E[rb][0]);
+    const float eb = __builtin_fmaf(E[rb][3], 1.f / 2048.f, E[rb][2]);
+    const float sa = __builtin_fmaf(fa, ea, __builtin_fmaf(D[rb][1], 1.f / 2048.f, D[rb][0]));
+    const float sb = __builtin_fmaf(fb, eb, __builtin_fmaf(D[rb][3], 1.f / 2048.f, D[rb][2]));
+    const uint32_t psc = L.upper ? h.w : h.y, pm = L.upper ? h.w : h.z;
+    const uint32_t scp = ((psc >> L.b0) & L.m1) | ((h.y >> (L.b0 + 2u)) & L.m2);
+    const uint32_t mp = ((pm >> L.mshift) & L.m1) | ((h.z >> (L.b0 + 2u)) & L.m2);
+    const float sca = (float)(scp & 0xFFu), scb = (float)((scp >> 8) & 0xFFu);
+    const float ma = (float)(mp & 0xFFu), mb = (float)((mp >> 8) & 0xFFu);
+    const float T = __builtin_fmaf(scb, sb, sca * sa);
+    const float M = __builtin_fmaf(mb, X.y, ma * X.x);
+    const float d = f16_ada(h.x & 0xFFFFu) * 16777216.f, dmin = f16_ada(h.x >> 16);
+    acc[rb] = __builtin_fmaf(__builtin_fmaf(d, T, -(dmin * M)), invS, acc[rb]);
   }
 }
 

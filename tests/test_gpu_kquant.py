@@ -352,7 +352,7 @@ def _x_variants(in_dim, gen):
 
 
 @pytest.mark.parametrize("engine", [0, 1], ids=["mfma", "valu"])
-@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K, aa.Q2_K], ids=["Q4_K", "Q6_K", "Q2_K"])
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K, aa.Q2_K, aa.Q5_K], ids=["Q4_K", "Q6_K", "Q2_K", "Q5_K"])
 def test_engines_activation_range(kind, engine, dev):
     """Both batch-1 engines for Q4_K and Q6_K against the oracle, over
     activations whose magnitudes span the f32 range, at shapes that take every
@@ -398,7 +398,7 @@ MFMA_SHAPE_CASES = [(64, 4096), (130, 4096), (1000, 2048), (4096, 4096), (300, 1
 
 @pytest.mark.parametrize("pipe", [0, 1, 2], ids=["plan", "prefetch", "sequential"])
 @pytest.mark.parametrize("rows", [1, 2], ids=["rows64", "rows16"])
-@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K, aa.Q2_K], ids=["Q4_K", "Q6_K", "Q2_K"])
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K, aa.Q2_K, aa.Q5_K], ids=["Q4_K", "Q6_K", "Q2_K", "Q5_K"])
 def test_mfma_workgroup_shapes(kind, rows, pipe, dev):
     dev.set_mfma_rows(rows)
     dev.lib.aspida_kq_set_mfma_pipeline(pipe)
