@@ -166,6 +166,28 @@ template <int RB> struct MvCol<Q5_K, RB> {
   }
 };
 
+// Q3_K (quarter c = 2 nh + g): qs chunk 2 + c (low-bit fields k = 0..3 of
+// elements l = 0..15) and hmask chunk g (their high bits 4 nh + k) of rows
+// 16 rb + n; the 12 scale bytes and d of row `lane` (RB = 4) or of the lane's
+// own row (RB = 1).
+template <int RB> struct MvCol<Q3_K, RB> {
+  uint4 q[RB], m[RB], sc;
+  uint32_t d;
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
+    const int n = lane & 15, c = lane >> 4;
+    const int hr = RB == 4 ? lane : 16 * rb0 + n;
+    const uint8_t* sp = grp + 6 * 1024 + 12 * hr;
+    sc = make_uint4(ld4(sp), ld4(sp + 4), ld4(sp + 8), 0u);
+    d = ld2(grp + 6 * 1024 + 768 + 2 * hr);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
+      q[rb] = ld16(r + (2 + c) * 1024);
+      m[rb] = ld16(r + (c & 1) * 1024);
+    }
+  }
+};
+
 // Q2_K (quarter c = 2 nh + g): qs chunk 1 + c (fields k = 0..3 of elements
 // l = 0..15) of rows 16 rb + n; the scale chunk 0 and d | dmin << 16 of row
 // `lane` (RB = 4) or of the lane's own row (RB = 1).
@@ -199,6 +221,10 @@ template <> struct MvHdr<Q6_K> {
   uint32_t d[64];
 };
 template <> struct MvHdr<Q2_K> {
+  uint4 sc[64];
+  uint32_t d[64];
+};
+template <> struct MvHdr<Q3_K> {
   uint4 sc[64];
   uint32_t d[64];
 };
@@ -454,6 +480,77 @@ __device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, c
     M = __builtin_fmaf((float)(b3 >> 4), X.w, M);
     const float d = f16_ada(DD[rb] & 0xFFFFu) * 16777216.f, dmin = f16_ada(DD[rb] >> 16);
     acc[rb] = __builtin_fmaf(__builtin_fmaf(d, T, -(dmin * M)), invS, acc[rb]);
+  }
+}
+
+// Q3_K (Decode_Q3K_Block, llm_dequant.adb:207-268): Q2_K's element layout
+// with a high bit, code = low2 + 4 hbit, w = d (sc - 32) (code - 4).  Since
+// code - 4 = low2 - 4 (1 - hbit), the low-bit fields take Q2_K's MFMAs and the
+// inverted high bits (hmask bit 4 nh + k clear) one more MFMA each against
+// the same fragments, left in place as the subnormals 2^(4nh+k-24) and scaled
+// back per lane by -4 2^-(4nh+k).  No sum of x is subtracted: a zero weight
+// (code 4) adds nothing to either sum, so a large activation there cannot
+// leave the matrix cores' truncation error of a cancelled term behind.
+template <int RB>
+__device__ __forceinline__ void mv_column(const MvCol<Q3_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q3_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  const int g = lane >> 4, n = lane & 15, nh = g >> 1, gg = g & 1;
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q3_K>(xv, L, xsum);
+  if (RB == 4) {
+    hdr->sc[lane] = c.sc;
+    hdr->d[lane] = c.d;
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint4 A[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) A[j] = img_frag(img, j, lane);
+  uint4 SC[RB];
+  uint32_t DD[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    SC[rb] = RB == 4 ? hdr->sc[16 * rb + n] : c.sc;
+    DD[rb] = RB == 4 ? hdr->d[16 * rb + n] : c.d;
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t hb = 0x00010001u << (4 * nh);
+  // Inverted high-bit sums carry 2^(4nh + k); code - 4 = low2 - 4 (1 - hbit).
+  const float fh = -4.f * __builtin_ldexpf(1.f, -4 * nh);
+  // One row block at a time: four accumulators live instead of 4 RB.
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    mf4 D0{0.f, 0.f, 0.f, 0.f}, D1 = D0, E0 = D0, E1 = D0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = dword_of(c.q[rb], j), t = w >> 8;
+      const uint32_t hm = ~dword_of(c.m[rb], j), ht = hm >> 8;
+      D0 = mfma_f16(A[j], make_uint4(w & 0x00030003u, t & 0x00030003u, w & 0x000C000Cu, t & 0x000C000Cu), D0);
+      E0 = mfma_f16(A[j], make_uint4(hm & hb, ht & hb, hm & (hb << 1), ht & (hb << 1)), E0);
+      D1 = mfma_f16(A[4 + j], make_uint4(w & 0x00300030u, t & 0x00300030u, w & 0x00C000C0u, t & 0x00C000C0u), D1);
+      E1 = mfma_f16(A[4 + j], make_uint4(hm & (hb << 2), ht & (hb << 2), hm & (hb << 3), ht & (hb << 3)), E1);
+    }
+    float cs[4];
+    cs[0] = __builtin_fmaf(fh, __builtin_fmaf(E0[1], 1.f / 2048.f, E0[0]), __builtin_fmaf(D0[1], 1.f / 2048.f, D0[0]));
+    cs[1] = __builtin_fmaf(fh * 0.5f, __builtin_fmaf(E0[3], 1.f / 2048.f, E0[2]),
+                           0.25f * __builtin_fmaf(D0[3], 1.f / 2048.f, D0[2]));
+    cs[2] = __builtin_fmaf(fh * 0.25f, __builtin_fmaf(E1[1], 1.f / 2048.f, E1[0]),
+                           0.0625f * __builtin_fmaf(D1[1], 1.f / 2048.f, D1[0]));
+    cs[3] = __builtin_fmaf(fh * 0.125f, __builtin_fmaf(E1[3], 1.f / 2048.f, E1[2]),
+                           0.015625f * __builtin_fmaf(D1[3], 1.f / 2048.f, D1[2]));
+    // 16 signed 6-bit scales (llm_dequant.adb:219-245): scale index 8 nh + 2k + g
+    // is byte (g + 2 (k & 1)) of dword k >> 1, high bits from dword 2.
+    const uint32_t sa[2] = {SC[rb].x, SC[rb].y}, tmp = SC[rb].z;
+    float T = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int kk = k >> 1;
+      const uint32_t bt = 8u * (uint32_t)(gg + 2 * (k & 1));
+      const uint32_t sc6 = bfe(sa[kk], bt + 4u * nh, 4) | (bfe(tmp, bt + 4u * nh + 2u * kk, 2) << 4);
+      T = __builtin_fmaf((float)((int)sc6 - 32), cs[k], T);
+    }
+    // cs[k] is sum (code - 4) x S in the codes' unit 2^-24.
+    acc[rb] = __builtin_fmaf(f16_ada(DD[rb]) * 16777216.f * T, invS, acc[rb]);
   }
 }
 

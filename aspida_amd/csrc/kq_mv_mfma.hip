@@ -155,7 +155,7 @@ static std::atomic<int> g_engine{0};
 void set_matvec_engine(int engine) { g_engine = engine; }
 
 bool matvec_mfma_takes(int kind) {
-  return (kind == Q4_K || kind == Q6_K || kind == Q2_K || kind == Q5_K) && g_engine.load() == 0;
+  return (kind == Q4_K || kind == Q6_K || kind == Q2_K || kind == Q5_K || kind == Q3_K) && g_engine.load() == 0;
 }
 
 // The kernel a plan runs: NW waves per workgroup and the column walk.
@@ -260,7 +260,7 @@ static hipError_t launch_mfma_kind(const uint8_t* w, int in_dim, int out_dim, co
     if (pipe == MV_ONE) KQ_GO(N, MV_ONE);                                                       \
     else if constexpr (N == 16) return hipErrorInvalidValue; /* 16 waves: one column only */    \
     else if (pipe == MV_SEQ) KQ_GO(N, MV_SEQ);                                                  \
-    else if constexpr (N <= 4 || (N == 8 && KIND != Q6_K && KIND != Q5_K)) KQ_GO(N, MV_PF);     \
+    else if constexpr (N <= 4 || (N == 8 && KIND != Q6_K && KIND != Q5_K && KIND != Q3_K)) KQ_GO(N, MV_PF); \
     else return hipErrorInvalidValue; /* two register sets: <= 8 waves, 4 for Q6_K/Q5_K */      \
     break;
   switch (p.nw) {
@@ -351,6 +351,7 @@ hipError_t launch_matvec_mfma(int kind, const void* P, int in_dim, int out_dim, 
     case Q6_K: return launch_mfma_kind<Q6_K>(w, in_dim, out_dim, x, y, part, count, s);
     case Q2_K: return launch_mfma_kind<Q2_K>(w, in_dim, out_dim, x, y, part, count, s);
     case Q5_K: return launch_mfma_kind<Q5_K>(w, in_dim, out_dim, x, y, part, count, s);
+    case Q3_K: return launch_mfma_kind<Q3_K>(w, in_dim, out_dim, x, y, part, count, s);
     default: return hipErrorNotSupported;
   }
 }

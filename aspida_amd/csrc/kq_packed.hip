@@ -267,8 +267,8 @@ PackedPlan mfma_plan(int kind, int in_dim, int out_dim) {
   }
   if (pipe == 1) p.seq = false;
   if (pipe == 2) p.seq = true;
-  // Prefetching waves (two register sets) fit at most 8 per workgroup, 4 for Q6_K and Q5_K.
-  if (p.spw > 1 && !p.seq && p.nw > (kind == Q6_K || kind == Q5_K ? 4 : 8)) p.seq = true;
+  // Prefetching waves (two register sets) fit at most 8 per workgroup, 4 for Q6_K, Q5_K and Q3_K.
+  if (p.spw > 1 && !p.seq && p.nw > (kind == Q6_K || kind == Q5_K || kind == Q3_K ? 4 : 8)) p.seq = true;
   return p;
 }
 
@@ -320,7 +320,7 @@ static PackedPlan mfma64_plan(int kind, int in_dim, int out_dim) {
 size_t packed_workspace_floats(int in_dim, int out_dim) {
   const int ks = std::max({packed_plan(in_dim, out_dim).ks, mfma_plan(Q4_K, in_dim, out_dim).ks,
                            mfma_plan(Q6_K, in_dim, out_dim).ks, mfma_plan(Q2_K, in_dim, out_dim).ks,
-                           mfma_plan(Q5_K, in_dim, out_dim).ks});
+                           mfma_plan(Q5_K, in_dim, out_dim).ks, mfma_plan(Q3_K, in_dim, out_dim).ks});
   return ks > 1 ? (size_t)ks * ((out_dim + 63) / 64) * 64 : 0;
 }
 
