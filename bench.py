@@ -16,8 +16,9 @@ captured once in a HIP graph and replayed.
 
 Printed: one JSON line (metric, value = tokens/s, roofline of the dominant
 kernel measured with HIP events on its stream, cpu_baseline = the C oracle of
-Aspida's CPU QMatVec on the host cores, and the per-kind batch-1 matvec table
-at the Llama-3-8B FFN shapes on cold HBM).
+Aspida's CPU QMatVec on the host cores, the per-kind batch-1 matvec table
+at the Llama-3-8B FFN shapes on cold HBM, the small-batch and MoE tables, and
+the same decode stream at Llama-3-70B shape: 80 layers, 44.4 GB per token).
 """
 import argparse
 import json
@@ -35,15 +36,22 @@ GIB = 1 << 30
 # Llama-3-8B: hidden 4096, FFN 14336, 32 q heads / 8 kv heads of 128, vocab 128256.
 HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
 Q4_K, Q6_K = 0, 1
+# The two weight streams: Llama-3-8B (the headline) and Llama-3-70B (hidden
+# 8192, FFN 28672, 64 q heads / 8 kv heads of 128, 80 layers; 44.4 GB resident).
+MODEL_8B = dict(name="llama3-8b", hidden=HIDDEN, ffn=FFN, kv=KV, vocab=VOCAB, layers=LAYERS,
+                stream_bytes=4_875_853_824)
+MODEL_70B = dict(name="llama3-70b", hidden=8192, ffn=28672, kv=1024, vocab=128256, layers=80,
+                 stream_bytes=44_383_027_200)
 
 
-def layer_plan():
+def layer_plan(m=MODEL_8B):
     """(name, kind, out_dim, in_dim, input) per weight matrix of one layer."""
-    return [("qk", Q4_K, HIDDEN + KV, HIDDEN, "h"),
-            ("v", Q6_K, KV, HIDDEN, "h"),
-            ("o", Q4_K, HIDDEN, HIDDEN, "att"),
-            ("gate_up", Q4_K, 2 * FFN, HIDDEN, "hn"),
-            ("down", Q6_K, HIDDEN, FFN, "act")]
+    h, f, kv = m["hidden"], m["ffn"], m["kv"]
+    return [("qk", Q4_K, h + kv, h, "h"),
+            ("v", Q6_K, kv, h, "h"),
+            ("o", Q4_K, h, h, "att"),
+            ("gate_up", Q4_K, 2 * f, h, "hn"),
+            ("down", Q6_K, h, f, "act")]
 
 
 # Launches of one layer: q|k and v share their input and run as one launch.
@@ -63,18 +71,20 @@ def parse():
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
+    ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B weight-stream line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
 
 
 class Decoder:
-    """Device-resident Llama-3-8B Q4_K_M weights, in the packed layout of the
-    batch-1 kernels, and the per-token launch list."""
+    """Device-resident Llama-3 Q4_K_M weights (8B by default), in the packed
+    layout of the batch-1 kernels, and the per-token launch list."""
 
-    def __init__(self, torch, aa, synth, seed, engine=0):
+    def __init__(self, torch, aa, synth, seed, engine=0, model=MODEL_8B):
         self.torch, self.dev = torch, aa.DeviceOps()
         self.aa = aa
+        self.m = m = model
         self.engine = engine
         self.dev.set_mv_engine(engine)
         g = torch.Generator(device="cuda")
@@ -87,14 +97,15 @@ class Decoder:
             torch.cuda.synchronize()
             return p
 
-        self.layers = [{name: packed(kind, out, inp) for name, kind, out, inp, _ in layer_plan()}
-                       for _ in range(LAYERS)]
-        self.head = packed(Q6_K, VOCAB, HIDDEN)
+        self.layers = [{name: packed(kind, out, inp) for name, kind, out, inp, _ in layer_plan(m)}
+                       for _ in range(m["layers"])]
+        self.head = packed(Q6_K, m["vocab"], m["hidden"])
         f = dict(device="cuda", dtype=torch.float32)
-        self.x = {"h": torch.randn(HIDDEN, generator=g, **f), "att": torch.randn(HIDDEN, generator=g, **f),
-                  "hn": torch.randn(HIDDEN, generator=g, **f), "act": torch.randn(FFN, generator=g, **f)}
-        self.y = {name: torch.empty(out, **f) for name, _, out, _, _ in layer_plan()}
-        self.logits = torch.empty(VOCAB, **f)
+        hid = m["hidden"]
+        self.x = {"h": torch.randn(hid, generator=g, **f), "att": torch.randn(hid, generator=g, **f),
+                  "hn": torch.randn(hid, generator=g, **f), "act": torch.randn(m["ffn"], generator=g, **f)}
+        self.y = {name: torch.empty(out, **f) for name, _, out, _, _ in layer_plan(m)}
+        self.logits = torch.empty(m["vocab"], **f)
 
     def build_chain(self):
         """The whole token as one resident chain (aspida_kq_chain_*): per layer
@@ -128,12 +139,12 @@ class Decoder:
     def launches(self):
         """Per launch, in decode order: a tuple of (kind, packed_ptr, in, out, x_key, y_ptr), one entry per
         matrix of the launch."""
-        plan = {name: (kind, out, inp, xk) for name, kind, out, inp, xk in layer_plan()}
+        plan = {name: (kind, out, inp, xk) for name, kind, out, inp, xk in layer_plan(self.m)}
         for L in self.layers:
             for names in LAYER_LAUNCHES:
                 yield tuple((plan[n][0], L[n].data_ptr(), plan[n][2], plan[n][1], plan[n][3], self.y[n].data_ptr())
                             for n in names)
-        yield ((Q6_K, self.head.data_ptr(), HIDDEN, VOCAB, "h", self.logits.data_ptr()),)
+        yield ((Q6_K, self.head.data_ptr(), self.m["hidden"], self.m["vocab"], "h", self.logits.data_ptr()),)
 
     def issue(self, op, stream):
         if len(op) == 1:
@@ -565,6 +576,25 @@ def main():
     moe = None if args.no_table else moe_table(torch, aa, synth, args.seed, stream)
     del dec
     torch.cuda.empty_cache()
+    big = None
+    if not args.no_70b:
+        # the 70B stream, 44.4 GB of distinct resident weights per token.
+        dec70 = Decoder(torch, aa, synth, args.seed + 70, args.mv_engine, MODEL_70B)
+        torch.cuda.synchronize()
+        steps70 = max(5, min(args.steps, 20))
+        w70, g70 = timed(dec70.step, steps70, min(args.warmup, 3))
+        b70 = MODEL_70B["stream_bytes"]
+        big = {"workload": "llama3-70b-q4_k_m-decode-weight-stream", "layers": MODEL_70B["layers"],
+               "hidden": MODEL_70B["hidden"], "ffn": MODEL_70B["ffn"], "kv_dim": MODEL_70B["kv"],
+               "vocab": MODEL_70B["vocab"], "weight_bytes_per_token": b70, "steps": steps70,
+               "tok_s": round(steps70 / w70, 2), "ms_per_step": round(w70 * 1e3 / steps70, 4),
+               "gpu_event_ms_per_step": round(g70 * 1e3 / steps70, 4),
+               "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / b70, 1),
+               "hbm_frac_of_stream": round(steps70 / w70 * b70 / (HBM_PEAK_GBS * 1e9), 4)}
+        print(f"# decode 70B (per-matrix launches): {big['tok_s']} tok/s "
+              f"({big['hbm_frac_of_stream']:.3f} of the HBM roofline)", file=sys.stderr, flush=True)
+        del dec70
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
@@ -588,14 +618,16 @@ def main():
         "kquant_matvec": table,
         "small_batch": small,
         "moe_layer": moe,
+        "decode_70b": big,
     }
-    assert dec_bytes_ok(stream_bytes), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"
+    assert dec_bytes_ok(MODEL_8B), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"
+    assert dec_bytes_ok(MODEL_70B), "weight stream size drifted from the Llama-3-70B Q4_K_M layout"
     print(json.dumps(line), flush=True)
 
 
-def dec_bytes_ok(expected):
-    per_layer = sum({Q4_K: 144, Q6_K: 210}[k] * o * (i // 256) for _, k, o, i, _ in layer_plan())
-    return LAYERS * per_layer + 210 * VOCAB * (HIDDEN // 256) == expected
+def dec_bytes_ok(m):
+    per_layer = sum({Q4_K: 144, Q6_K: 210}[k] * o * (i // 256) for _, k, o, i, _ in layer_plan(m))
+    return m["layers"] * per_layer + 210 * m["vocab"] * (m["hidden"] // 256) == m["stream_bytes"]
 
 
 if __name__ == "__main__":
