@@ -281,12 +281,21 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   // MI355X: Q4_K 4096x4096 4.3 us against 5.8 us on 64-row workgroups with
   // partial sums; 1024x14336 5.9 us on 64-row workgroups against 8.1 us.
   // Q2_K streams fewer bytes per column for the same arithmetic, so long
-  // column runs stay on 64-row workgroups (4096x14336: 8.6 us against 9.1).
+  // column runs stay on 64-row workgroups (4096x14336: 8.6 us against 9.1);
+  // so do Q3_K rows of more than 32 blocks (8192x28672: 29.4 us against 31.3).
+  // With more 16-row blocks than CUs, two blocks share a CU: 8 waves each
+  // keep both resident (Q4_K 8192x8192: 9.2 us against 10.1 with 16 waves;
+  // Q6_K 8192x28672: 35.7 against 36.8).
   const int nsb = in_dim / 256;
-  if (4L * ntiles <= 2L * cus && (nsb <= 16 || (4L * ntiles >= cus && kind != Q2_K))) return mfma16_plan(nsb);
-  // Very tall Q6_K matrices (the output head): 16-row workgroups of 8 waves
-  // walking 2+ columns each (128256x4096: 71.5 us against 77.3 on 64-row).
-  if (kind == Q6_K && ntiles >= 4L * cus) return mfma16_plan(nsb, 8);
+  if (4L * ntiles <= 2L * cus &&
+      (nsb <= 16 || (4L * ntiles >= cus && kind != Q2_K && (kind != Q3_K || nsb <= 32))))
+    return mfma16_plan(nsb, 4L * ntiles > cus ? 8 : 16);
+  // Tall matrices with long rows (the 70B FFN) and very tall Q6_K ones (the
+  // output heads): 16-row workgroups of 8 waves walking 2+ columns each
+  // (Q4_K 57344x8192: 47.9 us against 55.9 on 4-wave 64-row workgroups;
+  // Q6_K 128256x4096: 71.5 us against 77.3).
+  if ((kind == Q4_K || kind == Q6_K) && ntiles >= cus && (nsb >= 32 || (kind == Q6_K && ntiles >= 4L * cus)))
+    return mfma16_plan(nsb, 8);
   return mfma64_plan(kind, in_dim, out_dim);
 }
 

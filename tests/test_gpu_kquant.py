@@ -429,11 +429,14 @@ def test_packed_matvec_pair_workgroup_shapes(case, rows, dev):
         dev.set_mfma_rows(0)
 
 
-def test_tall_q6k_head_plan(dev):
-    """A Q6_K matrix of more than 1024 64-row tiles (the output head's shape
-    class) takes 16-row workgroups of 8 waves, 2 columns each, and matches
-    the oracle."""
-    kind, out_dim, in_dim = aa.Q6_K, 65600, 4096
+@pytest.mark.parametrize("kind,out_dim,in_dim,spw", [(aa.Q6_K, 65600, 4096, 2), (aa.Q4_K, 16448, 8192, 4),
+                                                     (aa.Q6_K, 8192, 28672, 14)],
+                         ids=["q6k-head-class", "q4k-70b-ffn-class", "q6k-70b-down"])
+def test_tall_plans_take_8_wave_16_row_groups(kind, out_dim, in_dim, spw, dev):
+    """Matrices of more 16-row blocks than CUs take 16-row workgroups of 8
+    waves walking `spw` columns each: a Q6_K matrix of more than 1024 64-row
+    tiles (the output head's class), a Q4_K one of 257 tiles with 32-block rows
+    (the 70B FFN's class) and the 70B down projection -- and match the oracle."""
     plan = dev.matvec_plan(kind, in_dim, out_dim)
-    assert plan[0] and plan[5] and plan[1] == 8 and plan[3] == 2, plan
-    _check_dev(dev, kind, out_dim, in_dim, 6161, "packed", f"Q6_K {out_dim}x{in_dim} plan={plan}")
+    assert plan[0] and plan[5] and plan[1] == 8 and plan[3] == spw, plan
+    _check_dev(dev, kind, out_dim, in_dim, 6161, "packed", f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} plan={plan}")
