@@ -189,12 +189,11 @@ struct MvWorkspace {
 // Y[batch][out] = X W^T over packed W on `st`.  Batch 1 is the matvec.
 // Otherwise, by g_mm_engine: 0 picks, 1 forces the multi-vector VALU kernel,
 // 2 the 64-vector and 3 the 16-vector MFMA kernel where the kind has one.
-// The pick (measured on MI355X, Q4_K): up to 4 vectors on VALU; 5-16 on the
-// 16-vector kernel; beyond 16 the 16-vector kernel in launches of 16 when
-// the matrix has at least MM16_MIN_UNITS (64-row tile, super-block column)
-// pairs to spread, else the 64-vector kernel, which then takes the batch in
-// fewer launches.  Q6_K: VALU up to 4, then the 64-vector kernel in launches
-// of up to 32.
+// The pick (measured on MI355X, Q4_K and Q6_K): up to 4 vectors on VALU;
+// 5-16 on the 16-vector kernel; beyond 16 the 16-vector kernel in launches
+// of 16 when the matrix has at least MM16_MIN_UNITS (64-row tile,
+// super-block column) pairs to spread, else the 64-vector kernel, which then
+// takes the batch in fewer launches (Q6_K: launches of up to 32).
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;

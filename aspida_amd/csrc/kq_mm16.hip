@@ -25,10 +25,17 @@
 // super-block columns, one after another; waves and workgroups meet as in
 // the batch-1 kernels (LDS, then the last-arriving workgroup, ascending).
 //
+// Q6_K's sixteen 16-element sub-blocks carry signed 8-bit scales, and
+// (q - 32) sc needs up to 13 bits, too many to fold into an exact f16 operand:
+// each sub-block is one v_mfma_f32_16x16x16_f16 of the raw 6-bit codes (B =
+// q 2^-24) against its own activation fragment, scaled in f32 on D, and the
+// -32 offset is one more K = 16 MFMA of the sub-block sums against the
+// scales (kq_mm16_ximage6 lays out that image: a fragment per sub-block).
+//
 // Accuracy as for the batch-1 MFMA kernels (kq_mv_mfma.hip): products exact,
 // sums in the matrix cores' f32.  Result per row: Decode_Q4K_Block
-// (src/llm/llm_dequant.adb:536-553) dotted with each vector (QMatMul,
-// llm_dequant.adb:808-932, once per vector).
+// (src/llm/llm_dequant.adb:536-553) or Decode_Q6K_Block (122-184) dotted with
+// each vector (QMatMul, llm_dequant.adb:808-932, once per vector).
 #include <algorithm>
 
 #include "kq_packed.h"
@@ -137,6 +144,73 @@ __global__ __launch_bounds__(256) void kq_mm16_ximage(const float* __restrict__ 
   }
 }
 
+// Q6_K's image: thread (b, u) holds sub-block u (elements 16 u .. + 15) of
+// vector b.  Fragment u, lane b + 16 kq: elements 4 kq + {0, 2, 1, 3} of the
+// sub-block, hi in .x .y, lo (times 2^11) in .z .w -- the x and y halves are
+// one K = 16 A operand each.  Fragment 16: the sub-block sums, lane b + 16 kq
+// holding sub-blocks 4 kq + {0, 2, 1, 3} in the same form.
+__global__ __launch_bounds__(256) void kq_mm16_ximage6(const float* __restrict__ X, int B, int in_dim,
+                                                       uint4* __restrict__ img, float* __restrict__ inv) {
+  __shared__ float sums[16][16];
+  const int t = threadIdx.x, b = t >> 4, u = t & 15, c = blockIdx.x;
+  float v[16];
+  if (b < B) {
+    const float4* p = reinterpret_cast<const float4*>(X + (size_t)b * in_dim + (size_t)c * 256 + 16 * u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 q = p[i];
+      v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = 0.f;
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(v[i]));
+  mx = fmaxf(mx, dpp_from<0x128>(mx, mx));  // row_ror:8
+  mx = fmaxf(mx, dpp_from<0x124>(mx, mx));  // row_ror:4
+  mx = fmaxf(mx, dpp_from<0x122>(mx, mx));  // row_ror:2
+  mx = fmaxf(mx, dpp_from<0x121>(mx, mx));  // row_ror:1
+  int e = 0;
+  const bool scaled = mx > 0.f && __builtin_isfinite(mx);
+  if (scaled) (void)frexpf(mx, &e);
+  const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
+  const float S = ldexpf(1.f, se);
+  if (u == 0) inv[(size_t)c * 16 + b] = ldexpf(1.f, -se);
+  float su = 0.f;
+  uint4* col = img + (size_t)c * MM16_NF * 64;
+#pragma unroll
+  for (int kq = 0; kq < 4; ++kq) {
+    const int ord[4] = {0, 2, 1, 3};
+    _Float16 hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = v[4 * kq + ord[i]] * S;
+      su += a;
+      hi[i] = (_Float16)a;
+      lo[i] = (_Float16)((a - (float)hi[i]) * 2048.f);
+    }
+    col[u * 64 + b + 16 * kq] = make_uint4(mm16_pack(hi[0], hi[1]), mm16_pack(hi[2], hi[3]),
+                                           mm16_pack(lo[0], lo[1]), mm16_pack(lo[2], lo[3]));
+  }
+  sums[b][u] = su;
+  __syncthreads();
+  if (t < 64) {
+    const int bb = t & 15, kq = t >> 4;
+    const int ord[4] = {0, 2, 1, 3};
+    _Float16 h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = sums[bb][4 * kq + ord[i]] * MM16_XSUM;
+      h[i] = (_Float16)a;
+      l[i] = (_Float16)((a - (float)h[i]) * 2048.f);
+    }
+    col[16 * 64 + t] = make_uint4(mm16_pack(h[0], h[1]), mm16_pack(h[2], h[3]), mm16_pack(l[0], l[1]),
+                                  mm16_pack(l[2], l[3]));
+  }
+}
+
 // ---- product ----------------------------------------------------------------
 
 struct Mm16Args {
@@ -156,6 +230,64 @@ __device__ __forceinline__ m16f4 mfma16(uint2 a, uint2 b, m16f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(m16h4, a), __builtin_bit_cast(m16h4, b), c, 0, 0, 0);
 }
 
+// acc[rb][i] (row 16 rb + n of the tile, vector 4 q + i) of every wave to Y:
+// waves meet in LDS, workgroups of a tile (ks > 1) through the partial sums
+// and the last-arriving workgroup, in ascending order.
+template <int NW>
+__device__ __forceinline__ void mm16_finish(const Mm16Args& a, const float (&acc)[4][4], float (&red)[NW][16][64],
+                                            unsigned& is_last, int w, int n, int q) {
+  const int tile = blockIdx.x, ks = gridDim.y;
+  // Each thread owns outputs o = threadIdx.x + 64 NW j (vector o / 64, row
+  // o % 64) and adds the waves in ascending order.
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[w][4 * q + i][16 * rb + n] = acc[rb][i];
+  __syncthreads();
+  constexpr int PER = 1024 / (64 * NW);
+  float outv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int o = threadIdx.x + 64 * NW * j, b = o >> 6, r = o & 63;
+    float t = red[0][b][r];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) t += red[k][b][r];
+    outv[j] = t;
+  }
+  if (ks > 1) {
+    const size_t ntiles = gridDim.x;
+    float* mine = a.part + ((size_t)blockIdx.y * ntiles + tile) * 1024;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      __hip_atomic_store(&mine[threadIdx.x + 64 * NW * j], outv[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      is_last = __hip_atomic_fetch_add(&a.count[(size_t)tile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks - 1)
+                    ? 1u
+                    : 0u;
+    __syncthreads();
+    if (!is_last) return;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int o = threadIdx.x + 64 * NW * j;
+      float t = 0.f;
+      for (int k = 0; k < ks; ++k)
+        t += __hip_atomic_load(a.part + ((size_t)k * ntiles + tile) * 1024 + o, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      outv[j] = t;
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.count[(size_t)tile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int o = threadIdx.x + 64 * NW * j, b = o >> 6, row = tile * 64 + (o & 63);
+    if (b < a.B && row < a.out_rows) a.Y[(size_t)b * a.out_rows + row] = outv[j];
+  }
+}
+
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void kq_mm16_q4k(Mm16Args a) {
   constexpr int GB = 64 * 144;
@@ -164,7 +296,7 @@ __global__ __launch_bounds__(64 * NW) void kq_mm16_q4k(Mm16Args a) {
   __shared__ unsigned is_last;
   const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = blockIdx.x, ks = gridDim.y;
+  const int tile = blockIdx.x;
   const int sb0 = (blockIdx.y * NW + w) * a.spw;
   // Scale extraction for lane group q's... every lane needs all 8 (sc, m) of
   // its row; mins go to the K = 16 MFMA as lane (n, q)'s four (q < 2).
@@ -247,56 +379,105 @@ __global__ __launch_bounds__(64 * NW) void kq_mm16_q4k(Mm16Args a) {
     }
   }
 
-  // acc[rb][i]: row 16 rb + n of the tile, vector 4 q + i.  Waves meet in
-  // LDS; each thread then owns outputs o = threadIdx.x + 64 NW j (vector o /
-  // 64, row o % 64) and adds the waves in ascending order.
+  mm16_finish<NW>(a, acc, red, is_last, w, n, q);
+}
+
+// Q6_K (Decode_Q6K_Block, llm_dequant.adb:122-184): sub-block sb = 8 h + 2 k
+// + t of row r takes, at its element l (0..15), the ql byte 16 (4 h + 2 (k %
+// 2) + t) + l (low nibble for k < 2, else high) and qh byte 16 (2 h + t) + l
+// (bits 2k, 2k + 1); in the packed layout those are byte l of chunks
+// 4 h + 2 (k % 2) + t and 8 + 2 h + t of the row.  Lane (n, kq) loads bytes
+// 4 kq .. + 3 of each chunk of row 16 rb + n: the B operand of every
+// sub-block's K = 16 MFMA.  The scale chunk (12) and d (the tail at 13 KB)
+// of row `lane` come in one coalesced load each, shared through LDS.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void kq_mm16_q6k(Mm16Args a) {
+  constexpr int GB = 64 * 210;
+  __shared__ uint4 hsc[NW][64];
+  __shared__ uint32_t hd[NW][64];
+  __shared__ float red[NW][16][64];
+  __shared__ unsigned is_last;
+  const int lane = threadIdx.x & 63, n = lane & 15, q = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = blockIdx.x;
+  const int sb0 = (blockIdx.y * NW + w) * a.spw;
+  float acc[4][4];
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[w][4 * q + i][16 * rb + n] = acc[rb][i];
-  __syncthreads();
-  constexpr int PER = 1024 / (64 * NW);
-  float outv[PER];
+    for (int i = 0; i < 4; ++i) acc[rb][i] = 0.f;
+  const m16f4 z4 = {0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < a.spw; ++s) {
+    const int col = sb0 + s;
+    const uint8_t* grp = a.P + ((size_t)tile * a.nsb + col) * GB;
+    asm volatile("" ::: "memory");  // this column's loads after the previous column's work
+    const uint4 h = ld16(grp + 12 * 1024 + lane * 16);
+    const uint32_t dd = ld2(grp + 13 * 1024 + 2 * lane);
+    uint32_t ql[4][8], qh[4][4];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int o = threadIdx.x + 64 * NW * j, b = o >> 6, r = o & 63;
-    float t = red[0][b][r];
+    for (int rb = 0; rb < 4; ++rb) {
+      const uint8_t* r = grp + (16 * rb + n) * 16 + 4 * q;
 #pragma unroll
-    for (int k = 1; k < NW; ++k) t += red[k][b][r];
-    outv[j] = t;
-  }
-  if (ks > 1) {
-    const size_t ntiles = gridDim.x;
-    float* mine = a.part + ((size_t)blockIdx.y * ntiles + tile) * 1024;
+      for (int c = 0; c < 8; ++c) ql[rb][c] = ld4(r + c * 1024);
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-      __hip_atomic_store(&mine[threadIdx.x + 64 * NW * j], outv[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      is_last = __hip_atomic_fetch_add(&a.count[(size_t)tile * COUNTER_STRIDE], 1u, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks - 1)
-                    ? 1u
-                    : 0u;
-    __syncthreads();
-    if (!is_last) return;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int o = threadIdx.x + 64 * NW * j;
-      float t = 0.f;
-      for (int k = 0; k < ks; ++k)
-        t += __hip_atomic_load(a.part + ((size_t)k * ntiles + tile) * 1024 + o, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-      outv[j] = t;
+      for (int c = 0; c < 4; ++c) qh[rb][c] = ld4(r + (8 + c) * 1024);
     }
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&a.count[(size_t)tile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+    const uint4* im = a.img + (size_t)col * MM16_NF * 64 + lane;
+    uint4 A[MM16_NF];
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int o = threadIdx.x + 64 * NW * j, b = o >> 6, row = tile * 64 + (o & 63);
-    if (b < a.B && row < a.out_rows) a.Y[(size_t)b * a.out_rows + row] = outv[j];
+    for (int f = 0; f < MM16_NF; ++f) A[f] = im[f * 64];
+    float4 iv;
+    __builtin_memcpy(&iv, __builtin_assume_aligned(a.inv + (size_t)col * 16 + 4 * q, 16), 16);
+    __builtin_amdgcn_wave_barrier();
+    hsc[w][lane] = h;
+    hd[w][lane] = dd;
+    __builtin_amdgcn_wave_barrier();
+    uint4 H[4];
+    uint32_t D[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      H[rb] = hsc[w][16 * rb + n];
+      D[rb] = hd[w][16 * rb + n];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float ivs[4] = {iv.x, iv.y, iv.z, iv.w};
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const uint32_t hs[4] = {H[rb].x, H[rb].y, H[rb].z, H[rb].w};
+      float t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sb = 0; sb < 16; ++sb) {
+        const int hh = sb >> 3, k = (sb >> 1) & 3, tt = sb & 1;
+        const uint32_t lw = ql[rb][4 * hh + 2 * (k & 1) + tt], hw = qh[rb][2 * hh + tt];
+        // 6-bit codes of elements 4 kq .. + 3 as bytes, then as f16 pairs
+        // {0, 2}, {1, 3} (the image's order): subnormals q 2^-24.
+        const uint32_t zc = (((k >> 1) ? (lw >> 4) : lw) & 0x0F0F0F0Fu) | (((hw >> (2 * k)) & 0x03030303u) << 4);
+        const uint2 bq = make_uint2(__builtin_amdgcn_perm(zc, zc, 0x0C020C00u), __builtin_amdgcn_perm(zc, zc, 0x0C030C01u));
+        const m16f4 dh = mfma16(make_uint2(A[sb].x, A[sb].y), bq, z4);
+        const m16f4 dl = mfma16(make_uint2(A[sb].z, A[sb].w), bq, z4);
+        const float sc = (float)(int)__builtin_amdgcn_sbfe(hs[sb >> 2], 8 * (sb & 3), 8);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[i] = __builtin_fmaf(sc, __builtin_fmaf(dl[i], 1.f / 2048.f, dh[i]), t[i]);
+      }
+      // The -32 offset: sum_sb sc_sb X_{b,sb}, lane (n, q) giving the scales
+      // of sub-blocks 4 q + {0, 2, 1, 3} as f16 (exact integers).
+      const uint32_t sw = hs[q];
+      _Float16 f[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) f[i] = (_Float16)(float)(int)__builtin_amdgcn_sbfe(sw, 8 * i, 8);
+      const uint2 bs = make_uint2(mm16_pack(f[0], f[2]), mm16_pack(f[1], f[3]));
+      const m16f4 mh = mfma16(make_uint2(A[16].x, A[16].y), bs, z4);
+      const m16f4 ml = mfma16(make_uint2(A[16].z, A[16].w), bs, z4);
+      const float d = f16_ada(D[rb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float off = __builtin_fmaf(ml[i], 1.f / 2048.f, mh[i]) * (32.f / MM16_XSUM);
+        acc[rb][i] = __builtin_fmaf(d * __builtin_fmaf(t[i], 16777216.f, -off), ivs[i], acc[rb][i]);
+      }
+    }
   }
+  mm16_finish<NW>(a, acc, red, is_last, w, n, q);
 }
 
 // ---- host -----------------------------------------------------------------
@@ -326,7 +507,7 @@ static PackedPlan mm16_plan(int in_dim, int out_dim) {
   return p;
 }
 
-bool mm16_kind(int kind) { return kind == Q4_K; }
+bool mm16_kind(int kind) { return kind == Q4_K || kind == Q6_K; }
 
 size_t mm16_workspace_bytes(int in_dim, int out_dim) {
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
@@ -348,13 +529,17 @@ hipError_t launch_matmul_mm16(int kind, const void* P, int in_dim, int out_dim, 
   uint4* img = (uint4*)wk;
   float* inv = (float*)(wk + (size_t)nsb * MM16_NF * 64 * 16);
   float* part = (float*)(wk + ((size_t)nsb * MM16_NF * 64 * 16 + (size_t)nsb * 16 * 4 + 255) / 256 * 256);
-  hipLaunchKernelGGL(kq_mm16_ximage, dim3(nsb), dim3(256), 0, s, X, batch, in_dim, img, inv);
+  if (kind == Q6_K)
+    hipLaunchKernelGGL(kq_mm16_ximage6, dim3(nsb), dim3(256), 0, s, X, batch, in_dim, img, inv);
+  else
+    hipLaunchKernelGGL(kq_mm16_ximage, dim3(nsb), dim3(256), 0, s, X, batch, in_dim, img, inv);
   const Mm16Args a{(const uint8_t*)P, nsb, out_dim, batch, p.spw, img, inv, Y, part, count};
   const dim3 grid(ntiles, p.ks);
+  const bool q6 = kind == Q6_K;
   switch (p.nw) {
-    case 4: hipLaunchKernelGGL(kq_mm16_q4k<4>, grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(kq_mm16_q4k<2>, grid, dim3(128), 0, s, a); break;
-    case 1: hipLaunchKernelGGL(kq_mm16_q4k<1>, grid, dim3(64), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(q6 ? kq_mm16_q6k<4> : kq_mm16_q4k<4>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(q6 ? kq_mm16_q6k<2> : kq_mm16_q4k<2>, grid, dim3(128), 0, s, a); break;
+    case 1: hipLaunchKernelGGL(q6 ? kq_mm16_q6k<1> : kq_mm16_q4k<1>, grid, dim3(64), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -348,13 +348,13 @@ def small_batch_table(torch, aa, synth, seed, stream):
 
 def small_batch_kernel(aa, kind, inp, out, B):
     """The kernel the library's default small-batch pick runs (matmul_packed in
-    aspidagpu.hip): the multi-vector VALU kernel up to 4 vectors; Q4_K then the
+    aspidagpu.hip): the multi-vector VALU kernel up to 4 vectors; then the
     16-vector MFMA kernel (above 16 vectors only for matrices of >= 2048
     64-row-by-256-column blocks), else the 64-vector MFMA kernel."""
     if B <= 4:
         return "kq_mm_packed_valu"
-    if kind == aa.Q4_K and (B <= 16 or (-(-out // 64)) * (inp // 256) >= 2048):
-        return "kq_mm16_q4k"
+    if B <= 16 or (-(-out // 64)) * (inp // 256) >= 2048:
+        return "kq_mm16_q4k" if kind == aa.Q4_K else "kq_mm16_q6k"
     return "kq_mm_mfma"
 
 

@@ -162,8 +162,8 @@ MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304
 
 @pytest.mark.parametrize("engine", [1, 2, 3])
 @pytest.mark.parametrize("case", MM_ENGINE_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
-def test_mm_engines_match_oracle(case, engine):
-    kind = aa.Q4_K
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+def test_mm_engines_match_oracle(kind, case, engine):
     batch, out_dim, in_dim = case
     gen = synth.rng(950 + batch + out_dim)
     w = synth.weight_np(kind, out_dim, in_dim, gen)
