@@ -67,7 +67,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--only", choices=["small", "moe", "kquant"],
+    ap.add_argument("--only", choices=["small", "moe", "kquant", "decode70"],
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
@@ -492,6 +492,54 @@ def _cpu_model():
     return "unknown"
 
 
+def timed_graph(torch, stream, step_fn, steps, warmup):
+    """Capture one token, replay `warmup` times, then time `steps` replays
+    (wall clock around synchronised replays, and HIP events on the stream)."""
+    with torch.cuda.stream(stream):
+        step_fn(stream.cuda_stream)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step_fn(stream.cuda_stream)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    del graph
+    return wall, e0.elapsed_time(e1) * 1e-3
+
+
+def decode_70b(torch, aa, synth, seed, stream, engine, steps, warmup):
+    """the Llama-3-70B Q4_K_M decode weight stream, 44.4 GB
+    of distinct resident weights per token, launched as the 8B stream is."""
+    dec70 = Decoder(torch, aa, synth, seed + 70, engine, MODEL_70B)
+    torch.cuda.synchronize()
+    steps70 = max(5, min(steps, 20))
+    w70, g70 = timed_graph(torch, stream, dec70.step, steps70, min(warmup, 3))
+    b70 = MODEL_70B["stream_bytes"]
+    big = {"workload": "llama3-70b-q4_k_m-decode-weight-stream", "layers": MODEL_70B["layers"],
+           "hidden": MODEL_70B["hidden"], "ffn": MODEL_70B["ffn"], "kv_dim": MODEL_70B["kv"],
+           "vocab": MODEL_70B["vocab"], "weight_bytes_per_token": b70, "steps": steps70,
+           "tok_s": round(steps70 / w70, 2), "ms_per_step": round(w70 * 1e3 / steps70, 4),
+           "gpu_event_ms_per_step": round(g70 * 1e3 / steps70, 4),
+           "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / b70, 1),
+           "hbm_frac_of_stream": round(steps70 / w70 * b70 / (HBM_PEAK_GBS * 1e9), 4)}
+    print(f"# decode 70B (per-matrix launches): {big['tok_s']} tok/s "
+          f"({big['hbm_frac_of_stream']:.3f} of the HBM roofline)", file=sys.stderr, flush=True)
+    del dec70
+    torch.cuda.empty_cache()
+    return big
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -506,6 +554,10 @@ def main():
         sys.exit(1)
     aa.load()                                       # fails loudly without the HIP library
     stream = torch.cuda.Stream()
+    if args.only == "decode70":
+        print(json.dumps({"decode_70b": decode_70b(torch, aa, synth, args.seed, stream, args.mv_engine, args.steps,
+                                                   args.warmup)}), flush=True)
+        return
     if args.only:
         fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
@@ -513,30 +565,7 @@ def main():
     dec = Decoder(torch, aa, synth, args.seed, args.mv_engine)
     torch.cuda.synchronize()
 
-    def timed(step_fn, steps, warmup):
-        """Capture one token, replay `warmup` times, then time `steps` replays
-        (wall clock around synchronised replays, and HIP events on the stream)."""
-        with torch.cuda.stream(stream):
-            step_fn(stream.cuda_stream)
-        stream.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            step_fn(stream.cuda_stream)
-        with torch.cuda.stream(stream):
-            for _ in range(warmup):
-                graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        with torch.cuda.stream(stream):
-            e0.record(stream)
-            for _ in range(steps):
-                graph.replay()
-            e1.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        del graph
-        return wall, e0.elapsed_time(e1) * 1e-3
+    timed = lambda step_fn, steps, warmup: timed_graph(torch, stream, step_fn, steps, warmup)
 
     # The token: per-matrix launches of the packed batch-1 kernels (q|k and v
     # share one), captured in one HIP graph.
@@ -576,25 +605,8 @@ def main():
     moe = None if args.no_table else moe_table(torch, aa, synth, args.seed, stream)
     del dec
     torch.cuda.empty_cache()
-    big = None
-    if not args.no_70b:
-        # the 70B stream, 44.4 GB of distinct resident weights per token.
-        dec70 = Decoder(torch, aa, synth, args.seed + 70, args.mv_engine, MODEL_70B)
-        torch.cuda.synchronize()
-        steps70 = max(5, min(args.steps, 20))
-        w70, g70 = timed(dec70.step, steps70, min(args.warmup, 3))
-        b70 = MODEL_70B["stream_bytes"]
-        big = {"workload": "llama3-70b-q4_k_m-decode-weight-stream", "layers": MODEL_70B["layers"],
-               "hidden": MODEL_70B["hidden"], "ffn": MODEL_70B["ffn"], "kv_dim": MODEL_70B["kv"],
-               "vocab": MODEL_70B["vocab"], "weight_bytes_per_token": b70, "steps": steps70,
-               "tok_s": round(steps70 / w70, 2), "ms_per_step": round(w70 * 1e3 / steps70, 4),
-               "gpu_event_ms_per_step": round(g70 * 1e3 / steps70, 4),
-               "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / b70, 1),
-               "hbm_frac_of_stream": round(steps70 / w70 * b70 / (HBM_PEAK_GBS * 1e9), 4)}
-        print(f"# decode 70B (per-matrix launches): {big['tok_s']} tok/s "
-              f"({big['hbm_frac_of_stream']:.3f} of the HBM roofline)", file=sys.stderr, flush=True)
-        del dec70
-        torch.cuda.empty_cache()
+    big = None if args.no_70b else decode_70b(torch, aa, synth, args.seed, stream, args.mv_engine, args.steps,
+                                              args.warmup)
 
     cpu = None
     if not args.no_cpu:
