@@ -283,13 +283,15 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   // Q2_K streams fewer bytes per column for the same arithmetic, so long
   // column runs stay on 64-row workgroups (4096x14336: 8.6 us against 9.1);
   // so do Q3_K rows of more than 32 blocks (8192x28672: 29.4 us against 31.3).
-  // With more 16-row blocks than CUs, two blocks share a CU: 8 waves each
-  // keep both resident (Q4_K 8192x8192: 9.2 us against 10.1 with 16 waves;
-  // Q6_K 8192x28672: 35.7 against 36.8).
+  // With more 16-row blocks than CUs, two blocks share a CU: when 16 waves
+  // would still walk several columns each, 8 waves keep both resident (Q4_K
+  // 8192x8192: 9.2 us against 10.1 with 16 waves; Q6_K 8192x28672: 35.7
+  // against 36.8); with rows of up to 16 blocks a column per wave stays
+  // better (q|k+v 6144x4096: 6.0 against 6.3).
   const int nsb = in_dim / 256;
   if (4L * ntiles <= 2L * cus &&
       (nsb <= 16 || (4L * ntiles >= cus && kind != Q2_K && (kind != Q3_K || nsb <= 32))))
-    return mfma16_plan(nsb, 4L * ntiles > cus ? 8 : 16);
+    return mfma16_plan(nsb, 4L * ntiles > cus && nsb > 16 ? 8 : 16);
   // Tall matrices with long rows (the 70B FFN) and very tall Q6_K ones (the
   // output heads): 16-row workgroups of 8 waves walking 2+ columns each
   // (Q4_K 57344x8192: 47.9 us against 55.9 on 4-wave 64-row workgroups;
