@@ -217,7 +217,8 @@ hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int b
       const int nb = std::min(step, batch - b0);
       const float* xb = X + (size_t)b0 * in_dim;
       float* yb = Y + (size_t)b0 * out_dim;
-      const hipError_t e = mm16 ? kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st)
+      const hipError_t e = mm16 ? kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st,
+                                                         batch <= step)
                                 : kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p,
                                                                 ws.count.p, st);
       if (e != hipSuccess) return e;

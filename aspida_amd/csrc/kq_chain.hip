@@ -147,7 +147,9 @@ __device__ __forceinline__ void chain_step(const ChainStepDev& st, int u, int u_
     return st.W + ((size_t)(ul / st.ks) * st.nsb + (c < st.nsb ? c : st.nsb - 1)) * GB;
   };
   R cur;
-  if (DB) cur = Packed<KIND>::load(col(u, 0), lane);
+  // Ordinary loads (not the streaming hint of the per-matrix kernels): the
+  // chain measured 542 tok/s with them and 518 without on the 8B decode.
+  if (DB) cur = Packed<KIND>::template load<false>(col(u, 0), lane);
   while (u < u_end) {
     const int ul = u - st.unit0, tile = ul / st.ks, cg = ul % st.ks;
     const int c0 = (cg * CH_NW + w) * spw;
@@ -169,18 +171,18 @@ __device__ __forceinline__ void chain_step(const ChainStepDev& st, int u, int u_
         // The next column: this unit's, else this wave's first of its next
         // unit (or, at the end of the step, the current one again).
         const uint8_t* np = j + 1 < nc ? col(u, j + 1) : un < u_end ? col(un, 0) : col(u, j);
-        const R nxt = Packed<KIND>::load(np, lane);
+        const R nxt = Packed<KIND>::template load<false>(np, lane);
         asm volatile("" ::: "memory");  // keep those loads issued here
         stage_x256(j == 0 ? x0 : x1, S.xst[w], lane, s16);
         acc += staged_dot<KIND>(cur, S.xst[w], s16);
         cur = nxt;
       } else {
-        const R r = Packed<KIND>::load(col(u, j), lane);
+        const R r = Packed<KIND>::template load<false>(col(u, j), lane);
         stage_x256(j == 0 ? x0 : x1, S.xst[w], lane, s16);
         acc += staged_dot<KIND>(r, S.xst[w], s16);
       }
     }
-    if (DB && nc == 0 && un < u_end) cur = Packed<KIND>::load(col(un, 0), lane);
+    if (DB && nc == 0 && un < u_end) cur = Packed<KIND>::template load<false>(col(un, 0), lane);
     // The waves meet once per unit; the partial buffer alternates with the
     // unit's parity, so the finishing wave reads it before anyone can write
     // it again (two barriers later).

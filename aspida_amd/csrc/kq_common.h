@@ -52,6 +52,21 @@ __device__ __forceinline__ float f16_ada(uint32_t bits16) {
 // fields only 2- or 4-byte aligned; gfx950 serves dword loads at any such
 // alignment and the compiler emits global_load_dwordx{1,2,4} for these.
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) { uint4 v; __builtin_memcpy(&v, p, 16); return v; }
+// A 16-byte-aligned load marked non-temporal: weights streamed once per
+// launch need not displace reusable lines in L2 and the Infinity Cache.
+typedef unsigned int kq_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16nt(const uint8_t* p) {
+  const kq_v4u v = __builtin_nontemporal_load(reinterpret_cast<const kq_v4u*>(__builtin_assume_aligned(p, 16)));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+typedef unsigned int kq_v2u __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ld8nt(const uint8_t* p) {
+  const kq_v2u v = __builtin_nontemporal_load(reinterpret_cast<const kq_v2u*>(__builtin_assume_aligned(p, 8)));
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld4nt(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(p, 4)));
+}
 __device__ __forceinline__ uint2 ld8(const uint8_t* p) { uint2 v; __builtin_memcpy(&v, p, 8); return v; }
 __device__ __forceinline__ uint32_t ld4(const uint8_t* p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
 __device__ __forceinline__ uint32_t ld2(const uint8_t* p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }

@@ -94,7 +94,7 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
 bool mm16_kind(int kind);
 size_t mm16_workspace_bytes(int in_dim, int out_dim);
 hipError_t launch_matmul_mm16(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
-                              void* work, unsigned* count, hipStream_t s);
+                              void* work, unsigned* count, hipStream_t s, bool stream_once);
 
 // ggml layout -> packed (unpack = false) or back (unpack = true).
 // Y[b][out] = W X[b] for nb <= 8 vectors over packed W on VALU

@@ -196,8 +196,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_
       const int col = w + c * NW;
       const float4* xc = reinterpret_cast<const float4*>(x + (size_t)col * 256) + lane;
       float4 xv = xc[(size_t)(S.jobs[it.j0] / slots) * (a.dim / 4)];
-      typename Packed<KIND>::R rg = Packed<KIND>::load(G + (size_t)col * GB, lane);
-      typename Packed<KIND>::R ru = Packed<KIND>::load(U + (size_t)col * GB, lane);
+      // Ordinary loads: an expert tile of more than MOE_JPW jobs is read again
+      // by the adjacent items, and the caches serve those repeats.
+      typename Packed<KIND>::R rg = Packed<KIND>::template load<false>(G + (size_t)col * GB, lane);
+      typename Packed<KIND>::R ru = Packed<KIND>::template load<false>(U + (size_t)col * GB, lane);
 #pragma unroll 1
       for (int j = 0; j < it.nj; ++j) {
         const float4 cur = xv;
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(64 * NW) void moe_down(MoeGroupedArgs a, int cpw, c
       const int col = w + c * NW;
       const float4* hc = reinterpret_cast<const float4*>(h + (size_t)col * 256) + lane;
       float4 hv = hc[(size_t)S.jobs[it.j0] * (a.I / 4)];
-      typename Packed<KIND>::R rd = Packed<KIND>::load(D + (size_t)col * GB, lane);
+      typename Packed<KIND>::R rd = Packed<KIND>::template load<false>(D + (size_t)col * GB, lane);
 #pragma unroll 1
       for (int j = 0; j < it.nj; ++j) {
         const float4 cur = hv;

@@ -115,12 +115,12 @@ template <int RB> struct MvCol<Q4_K, RB> {
   uint4 h, a[RB], b[RB];
   __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
     const int n = lane & 15, g = lane >> 4;
-    h = ld16(grp + (RB == 4 ? lane : 16 * rb0 + n) * 16);
+    h = ld16nt(grp + (RB == 4 ? lane : 16 * rb0 + n) * 16);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
-      a[rb] = ld16(r + (1 + 2 * g) * 1024);
-      b[rb] = ld16(r + (2 + 2 * g) * 1024);
+      a[rb] = ld16nt(r + (1 + 2 * g) * 1024);
+      b[rb] = ld16nt(r + (2 + 2 * g) * 1024);
     }
   }
 };
@@ -134,14 +134,14 @@ template <int RB> struct MvCol<Q6_K, RB> {
   __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
     const int n = lane & 15, g = lane >> 4, h = g >> 1, t = g & 1;
     const int hr = RB == 4 ? lane : 16 * rb0 + n;
-    sc = ld16(grp + 12 * 1024 + hr * 16);
+    sc = ld16nt(grp + 12 * 1024 + hr * 16);
     d = ld2(grp + 13 * 1024 + hr * 2);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
-      a[rb] = ld16(r + (4 * h + t) * 1024);
-      b[rb] = ld16(r + (4 * h + 2 + t) * 1024);
-      q[rb] = ld16(r + (8 + 2 * h + t) * 1024);
+      a[rb] = ld16nt(r + (4 * h + t) * 1024);
+      b[rb] = ld16nt(r + (4 * h + 2 + t) * 1024);
+      q[rb] = ld16nt(r + (8 + 2 * h + t) * 1024);
     }
   }
 };
@@ -154,14 +154,14 @@ template <int RB> struct MvCol<Q5_K, RB> {
   uint4 h, a[RB], b[RB], ha[RB], hb[RB];
   __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
     const int n = lane & 15, g = lane >> 4;
-    h = ld16(grp + (RB == 4 ? lane : 16 * rb0 + n) * 16);
+    h = ld16nt(grp + (RB == 4 ? lane : 16 * rb0 + n) * 16);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
-      a[rb] = ld16(r + (3 + 2 * g) * 1024);
-      b[rb] = ld16(r + (4 + 2 * g) * 1024);
-      ha[rb] = ld16(r + 1 * 1024);
-      hb[rb] = ld16(r + 2 * 1024);
+      a[rb] = ld16nt(r + (3 + 2 * g) * 1024);
+      b[rb] = ld16nt(r + (4 + 2 * g) * 1024);
+      ha[rb] = ld16nt(r + 1 * 1024);
+      hb[rb] = ld16nt(r + 2 * 1024);
     }
   }
 };
@@ -182,8 +182,8 @@ template <int RB> struct MvCol<Q3_K, RB> {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       const uint8_t* r = grp + (16 * (rb0 + rb) + n) * 16;
-      q[rb] = ld16(r + (2 + c) * 1024);
-      m[rb] = ld16(r + (c & 1) * 1024);
+      q[rb] = ld16nt(r + (2 + c) * 1024);
+      m[rb] = ld16nt(r + (c & 1) * 1024);
     }
   }
 };
@@ -197,10 +197,10 @@ template <int RB> struct MvCol<Q2_K, RB> {
   __device__ __forceinline__ void load(const uint8_t* __restrict__ grp, int lane, int rb0) {
     const int n = lane & 15, c = lane >> 4;
     const int hr = RB == 4 ? lane : 16 * rb0 + n;
-    sc = ld16(grp + hr * 16);
+    sc = ld16nt(grp + hr * 16);
     d = ld4(grp + 5 * 1024 + hr * 4);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) q[rb] = ld16(grp + (1 + c) * 1024 + (16 * (rb0 + rb) + n) * 16);
+    for (int rb = 0; rb < RB; ++rb) q[rb] = ld16nt(grp + (1 + c) * 1024 + (16 * (rb0 + rb) + n) * 16);
   }
 };
 

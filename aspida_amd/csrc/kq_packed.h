@@ -52,12 +52,13 @@ __host__ __device__ constexpr int packed_offset(int kind, int r, int b) {
   }
 }
 
-// Whole-chunk loads of row `lane`'s super-block from the group at g.
-template <int C>
+// Whole-chunk loads of row `lane`'s super-block from the group at g;
+// non-temporal (NT) when the launch reads the group once.
+template <int C, bool NT = true>
 __device__ __forceinline__ void load_chunks(const uint8_t* g, int lane, uint4 (&ch)[C]) {
   const uint8_t* p = g + lane * 16;
 #pragma unroll
-  for (int k = 0; k < C; ++k) ch[k] = ld16(p + k * 1024);
+  for (int k = 0; k < C; ++k) ch[k] = NT ? ld16nt(p + k * 1024) : ld16(p + k * 1024);
 }
 
 // Make the compiler treat a register image as changed (it is not): a loop
@@ -76,9 +77,10 @@ __device__ __forceinline__ void opaque_regs(R& r) {
 
 template <> struct Packed<Q4_K> {
   struct R { uint4 ch[9]; };
+  template <bool NT = true>
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
     R r;
-    load_chunks<9>(g, lane, r.ch);
+    load_chunks<9, NT>(g, lane, r.ch);
     return r;
   }
   __device__ static __forceinline__ Block<Q4_K>::W quarter(const R& r, int q) {
@@ -88,9 +90,10 @@ template <> struct Packed<Q4_K> {
 
 template <> struct Packed<Q5_K> {
   struct R { uint4 ch[11]; };
+  template <bool NT = true>
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
     R r;
-    load_chunks<11>(g, lane, r.ch);
+    load_chunks<11, NT>(g, lane, r.ch);
     return r;
   }
   __device__ static __forceinline__ Block<Q5_K>::W quarter(const R& r, int q) {
@@ -100,9 +103,10 @@ template <> struct Packed<Q5_K> {
 
 template <> struct Packed<Q6_K> {
   struct R { uint4 ch[13]; uint32_t d; };
+  template <bool NT = true>
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
     R r;
-    load_chunks<13>(g, lane, r.ch);
+    load_chunks<13, NT>(g, lane, r.ch);
     r.d = ld2(g + 13 * 1024 + 2 * lane);
     return r;
   }
@@ -116,9 +120,10 @@ template <> struct Packed<Q6_K> {
 
 template <> struct Packed<Q3_K> {
   struct R { uint4 ch[6]; uint4 s; uint32_t d; };
+  template <bool NT = true>
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
     R r;
-    load_chunks<6>(g, lane, r.ch);
+    load_chunks<6, NT>(g, lane, r.ch);
     const uint8_t* sp = g + 6 * 1024 + 12 * lane;
     r.s = make_uint4(ld4(sp), ld4(sp + 4), ld4(sp + 8), 0u);
     r.d = ld2(g + 6 * 1024 + 768 + 2 * lane);
@@ -133,9 +138,10 @@ template <> struct Packed<Q3_K> {
 
 template <> struct Packed<Q2_K> {
   struct R { uint4 ch[5]; uint32_t d; };
+  template <bool NT = true>
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
     R r;
-    load_chunks<5>(g, lane, r.ch);
+    load_chunks<5, NT>(g, lane, r.ch);
     r.d = ld4(g + 5 * 1024 + 4 * lane);
     return r;
   }
@@ -148,9 +154,10 @@ template <> struct Packed<Q2_K> {
 
 template <> struct Packed<Q8_0> {
   struct R { uint4 ch[17]; };
+  template <bool NT = true>
   __device__ static __forceinline__ R load(const uint8_t* g, int lane) {
     R r;
-    load_chunks<17>(g, lane, r.ch);
+    load_chunks<17, NT>(g, lane, r.ch);
     return r;
   }
   // Quarter c owns blocks 2c and 2c+1: codes in chunks 4c..4c+3, scales in
