@@ -337,6 +337,11 @@ size_t packed_workspace_floats(int in_dim, int out_dim) {
 
 size_t packed_counters(int out_dim) { return (size_t)(out_dim + 63) / 64 * COUNTER_STRIDE; }
 
+// Whether the prefetching walk (two weight register sets) fits without
+// spilling: not for Q8_0's 17 chunks per row at 16 waves per workgroup, which
+// walk their columns one after another instead.
+static constexpr bool pf_fits(int ka, int kb, int nw) { return !(nw == 16 && (ka == Q8_0 || kb == Q8_0)); }
+
 template <int KIND>
 static hipError_t launch_mvp_kind(const uint8_t* P, int in_dim, int out_dim, const float* x, float* y, float* part,
                                   unsigned* count, hipStream_t s) {
@@ -346,12 +351,14 @@ static hipError_t launch_mvp_kind(const uint8_t* P, int in_dim, int out_dim, con
   switch (p.nw) {
 #define KQ_MVP(N)                                                                                              \
   case N:                                                                                                      \
-    if (p.spw > 1)                                                                                             \
-      hipLaunchKernelGGL((kq_mv_packed<KIND, N, true>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw, \
-                         part, count);                                                                         \
-    else                                                                                                       \
-      hipLaunchKernelGGL((kq_mv_packed<KIND, N, false>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw, \
-                         part, count);                                                                         \
+    if constexpr (pf_fits(KIND, KIND, N))                                                                      \
+      if (p.spw > 1) {                                                                                         \
+        hipLaunchKernelGGL((kq_mv_packed<KIND, N, true>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y,      \
+                           p.spw, part, count);                                                                \
+        break;                                                                                                 \
+      }                                                                                                        \
+    hipLaunchKernelGGL((kq_mv_packed<KIND, N, false>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, x, y, p.spw,  \
+                       part, count);                                                                           \
     break;
     KQ_MVP(16) KQ_MVP(8) KQ_MVP(4) KQ_MVP(2) KQ_MVP(1)
 #undef KQ_MVP
@@ -398,12 +405,14 @@ static hipError_t launch_mv2_pair(const void* Pa, int out_a, float* ya, const vo
   switch (p.nw) {
 #define KQ_MV2(N)                                                                                             \
   case N:                                                                                                     \
-    if (p.spw > 1)                                                                                            \
-      hipLaunchKernelGGL((kq_mv_packed2<KA, KB, N, true>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb, \
-                         tiles_a, nsb, x, p.spw, part, count);                                                \
-    else                                                                                                      \
-      hipLaunchKernelGGL((kq_mv_packed2<KA, KB, N, false>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb, \
-                         tiles_a, nsb, x, p.spw, part, count);                                                \
+    if constexpr (pf_fits(KA, KB, N))                                                                         \
+      if (p.spw > 1) {                                                                                        \
+        hipLaunchKernelGGL((kq_mv_packed2<KA, KB, N, true>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, \
+                           yb, tiles_a, nsb, x, p.spw, part, count);                                          \
+        break;                                                                                                \
+      }                                                                                                       \
+    hipLaunchKernelGGL((kq_mv_packed2<KA, KB, N, false>), grid, dim3(64 * N), 0, s, a, out_a, ya, b, out_b, yb, \
+                       tiles_a, nsb, x, p.spw, part, count);                                                  \
     break;
     KQ_MV2(16) KQ_MV2(8) KQ_MV2(4) KQ_MV2(2) KQ_MV2(1)
 #undef KQ_MV2

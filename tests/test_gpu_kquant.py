@@ -440,3 +440,14 @@ def test_tall_plans_take_8_wave_16_row_groups(kind, out_dim, in_dim, spw, dev):
     plan = dev.matvec_plan(kind, in_dim, out_dim)
     assert plan[0] and plan[5] and plan[1] == 8 and plan[3] == spw, plan
     _check_dev(dev, kind, out_dim, in_dim, 6161, "packed", f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} plan={plan}")
+
+
+def test_q8_0_sixteen_wave_column_walk(dev):
+    """Q8_0 on 16-wave workgroups walking several columns per wave (more than
+    255 tiles, rows of 32 super-blocks) takes the walk without prefetching --
+    the prefetching one does not fit Q8_0's registers at 16 waves -- and
+    matches the oracle."""
+    kind, out_dim, in_dim = aa.Q8_0, 16448, 8192
+    plan = dev.matvec_plan(kind, in_dim, out_dim)
+    assert not plan[0] and plan[1] == 16 and plan[3] == 2, plan
+    _check_dev(dev, kind, out_dim, in_dim, 8080, "packed", f"Q8_0 {out_dim}x{in_dim} plan={plan}")
