@@ -118,14 +118,19 @@ static hipError_t launch_multi_kind(const uint8_t* P, int in_dim, int out_dim, i
   const dim3 grid((out_dim + 63) / 64, p.ks);
   const int nsb = in_dim / 256;
   switch (p.nw) {
+// The prefetching walk holds two weight register sets: at 16 waves per
+// workgroup Q6_K and Q8_0 spill with it (16-77 registers), so they walk their
+// columns one after another.
 #define KQ_MM(N)                                                                                                 \
   case N:                                                                                                        \
-    if (p.spw > 1)                                                                                               \
-      hipLaunchKernelGGL((kq_mm_packed_valu<KIND, N, BMAX, true>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, X, \
-                         in_dim, nb, Y, p.spw, part, count);                                                     \
-    else                                                                                                         \
-      hipLaunchKernelGGL((kq_mm_packed_valu<KIND, N, BMAX, false>), grid, dim3(64 * N), 0, s, P, nsb, out_dim,  \
-                         X, in_dim, nb, Y, p.spw, part, count);                                                  \
+    if constexpr (!(N == 16 && (KIND == Q6_K || KIND == Q8_0)))                                                  \
+      if (p.spw > 1) {                                                                                           \
+        hipLaunchKernelGGL((kq_mm_packed_valu<KIND, N, BMAX, true>), grid, dim3(64 * N), 0, s, P, nsb, out_dim,  \
+                           X, in_dim, nb, Y, p.spw, part, count);                                                \
+        break;                                                                                                   \
+      }                                                                                                          \
+    hipLaunchKernelGGL((kq_mm_packed_valu<KIND, N, BMAX, false>), grid, dim3(64 * N), 0, s, P, nsb, out_dim, X,  \
+                       in_dim, nb, Y, p.spw, part, count);                                                       \
     break;
     KQ_MM(16) KQ_MM(8) KQ_MM(4) KQ_MM(2) KQ_MM(1)
 #undef KQ_MM

@@ -290,3 +290,19 @@ def test_reference_harness_against_this_library():
     print(r.stdout[-3000:])
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     assert "PASS" in r.stdout
+
+
+@pytest.mark.parametrize("kind", [aa.Q6_K, aa.Q8_0], ids=["Q6_K", "Q8_0"])
+def test_multi_vector_sixteen_wave_column_walk(kind):
+    """Three vectors (the multi-vector kernel's range) over more than 255
+    tiles with rows of 32 super-blocks: 16-wave workgroups walking two columns
+    per wave without prefetching (the prefetching walk does not fit Q6_K's and
+    Q8_0's registers at 16 waves)."""
+    gen = synth.rng(1616 + kind)
+    batch, out_dim, in_dim = 3, 16448, 8192
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
+    assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
+                        what=f"{aa.KIND_NAMES[kind]} B={batch} {out_dim}x{in_dim}")
