@@ -220,7 +220,7 @@ hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int b
       const hipError_t e = mm16 ? kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st,
                                                          batch <= step)
                                 : kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p,
-                                                                ws.count.p, st);
+                                                                ws.count.p, st, batch <= step);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;

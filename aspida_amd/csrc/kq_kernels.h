@@ -86,7 +86,7 @@ hipError_t launch_matvec2_packed(int kind_a, const void* Pa, int out_a, float* y
 bool mfma_kind(int kind);
 size_t mfma_workspace_bytes(int in_dim, int out_dim, int batch);
 hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X,
-                                     float* Y, void* work, unsigned* count, hipStream_t s);
+                                     float* Y, void* work, unsigned* count, hipStream_t s, bool stream_once);
 
 // Up to 16 activation rows per launch on MFMA, dense in rows and vectors
 // (kq_mm16.hip): kinds it takes, workspace bytes (activation images and

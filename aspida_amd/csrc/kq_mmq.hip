@@ -145,6 +145,8 @@ struct MmArgs {
   float* Y;           // [B][out_dim]
   float* part;        // [ks][ntiles][Bp][64] partial sums (ks > 1)
   unsigned* count;    // [ntiles] arrival counters
+  int nt;             // 1: weights read by this launch only (Q4_K: non-temporal loads;
+                      // Q6_K measured slower with the per-load choice, 29.6 -> 30.1 us)
 };
 
 // Workgroup = 4 waves over one 64-row tile and a range of spw super-block
@@ -296,9 +298,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   const int tile = blockIdx.x;
   auto load_w = [&](int s, Q4Regs& r) {
     const uint8_t* g = a.P + ((size_t)tile * a.nsb + s) * GB;
-    r.h = ld16(g + 16 * row);
+    r.h = a.nt ? ld16nt(g + 16 * row) : ld16(g + 16 * row);
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) r.wc[gq] = ld8(g + (1 + 2 * gq + (q >> 1)) * 1024 + 16 * row + 8 * (q & 1));
+    for (int gq = 0; gq < 4; ++gq) {
+      const uint8_t* src = g + (1 + 2 * gq + (q >> 1)) * 1024 + 16 * row + 8 * (q & 1);
+      r.wc[gq] = a.nt ? ld8nt(src) : ld8(src);
+    }
   };
   f4 acc[MB];
 #pragma unroll
@@ -509,7 +514,7 @@ size_t mfma_workspace_bytes(int in_dim, int out_dim, int batch) {
 }
 
 hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X,
-                                     float* Y, void* work, unsigned* count, hipStream_t s) {
+                                     float* Y, void* work, unsigned* count, hipStream_t s, bool stream_once) {
   if (!mfma_kind(kind)) return hipErrorNotSupported;
   if (batch < 1 || batch > 64 || in_dim % 256 || out_dim <= 0) return hipErrorInvalidValue;
   const int bp = mm_bpad(batch), nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
@@ -527,7 +532,7 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
     hipLaunchKernelGGL(kq_xsplit<32>, dim3(bp), dim3(1024), 0, s, X, batch, in_dim, xh, xl, sh, sl, inv);
   else
     hipLaunchKernelGGL(kq_xsplit<16>, dim3(bp), dim3(1024), 0, s, X, batch, in_dim, xh, xl, sh, sl, inv);
-  const MmArgs a{(const uint8_t*)P, nsb, out_dim, batch, spw, xh, xl, sh, sl, inv, Y, part, count};
+  const MmArgs a{(const uint8_t*)P, nsb, out_dim, batch, spw, xh, xl, sh, sl, inv, Y, part, count, stream_once ? 1 : 0};
   const dim3 grid(ntiles, ks);
   // One column per workgroup needs a single activation buffer: half the LDS,
   // so more workgroups are resident at once.
