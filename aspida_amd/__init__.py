@@ -79,6 +79,7 @@ def load(path=None):
         "aspida_kq_chain_check": (I, [P]),
         "aspida_kq_chain_workgroups": (I, [P]),
         "aspida_kq_chain_destroy": (None, [P]),
+        "aspida_kq_matmul_workspace": (I, [I, I, I, I, P, P]),
         "aspida_kq_set_packed_plan": (I, [I, I]),
         "aspida_kq_set_mv_engine": (I, [I]),
         "aspida_kq_set_mfma_rows": (I, [I]),

@@ -21,6 +21,7 @@
 #include <atomic>
 #include <cstdint>
 #include <mutex>
+#include <shared_mutex>
 #include <unordered_map>
 #include <vector>
 
@@ -63,89 +64,159 @@ long need_bytes(int kind, int in_dim, int rows) {
 }
 
 // ---- VRAM weight cache keyed by host pointer --------------------------------
+//
+// Two mirrors per host pointer: the ggml layout (ggml bytes) and the packed
+// layout of the batch-1 kernels.  A host-ABI call holds g_wmu shared from its
+// lookup until its stream has been synchronised, so no mirror it uses can be
+// freed or re-packed under it: aspida_gpu_free_weight and every upload or
+// re-pack take g_wmu exclusively and so wait for the calls in flight.
 
 struct WEnt {
   void* d;
   long bytes;
 };
-std::mutex g_wmu;
-std::unordered_map<const void*, WEnt> g_wcache;
-
-// Device mirror of [w, w + bytes) in the ggml layout.  A cached copy at least
-// that large is reused; a smaller one is replaced.
-void* weight(const void* w, long bytes) {
-  std::lock_guard<std::mutex> lk(g_wmu);
-  auto it = g_wcache.find(w);
-  if (it != g_wcache.end()) {
-    if (it->second.bytes >= bytes) return it->second.d;
-    (void)hipFree(it->second.d);
-    g_wcache.erase(it);
-  }
-  void* d = nullptr;
-  if (check(hipMalloc(&d, (size_t)bytes), "weight upload: hipMalloc")) return nullptr;
-  if (check(hipMemcpy(d, w, (size_t)bytes, hipMemcpyHostToDevice), "weight upload: hipMemcpy")) {
-    (void)hipFree(d);
-    return nullptr;
-  }
-  g_wcache[w] = {d, bytes};
-  return d;
-}
-
-// Device mirror of the matrix at w in the lane-interleaved layout of the
-// batch-1 kernels, packed on the device from a temporary ggml copy.  For n > 1
-// the host holds n matrices src_stride bytes apart (MoE experts) and the
-// mirror holds them packed_bytes apart.  Keyed by host pointer; a different
-// kind, shape or count for the same pointer re-packs.
+// Packed mirror: n matrices of kind / in_dim / out_dim, packed_bytes apart.
 struct PEnt {
   void* d;
   int kind, in_dim, out_dim, n;
 };
+std::shared_mutex g_wmu;
+std::unordered_map<const void*, WEnt> g_wcache;
 std::unordered_map<const void*, PEnt> g_pcache;
 
-void* packed_weight(const void* w, int kind, int in_dim, int out_dim, int n = 1, size_t src_stride = 0) {
-  std::lock_guard<std::mutex> lk(g_wmu);
-  auto it = g_pcache.find(w);
+// One weight a call needs in HBM: the ggml mirror of [w, w + bytes), or
+// (packed) the packed mirror of n matrices the host holds src_stride bytes
+// apart (MoE experts; n = 1 for a plain matrix).
+struct WReq {
+  const void* w = nullptr;
+  bool packed = false;
+  long bytes = 0;
+  int kind = 0, in_dim = 0, out_dim = 0, n = 1;
+  size_t src_stride = 0;
+  void* d = nullptr;  // the mirror, once acquired
+};
+
+WReq ggml_req(const void* w, long bytes) {
+  WReq r;
+  r.w = w;
+  r.bytes = bytes;
+  return r;
+}
+
+WReq packed_req(const void* w, int kind, int in_dim, int out_dim, int n = 1, size_t src_stride = 0) {
+  WReq r;
+  r.w = w;
+  r.packed = true;
+  r.kind = kind;
+  r.in_dim = in_dim;
+  r.out_dim = out_dim;
+  r.n = n;
+  r.src_stride = src_stride;
+  return r;
+}
+
+// The cached mirror satisfying r, or null (g_wmu held, either way).  A ggml
+// mirror at least r.bytes long serves; a packed one must match exactly.
+void* lookup(const WReq& r) {
+  if (!r.packed) {
+    auto it = g_wcache.find(r.w);
+    return it != g_wcache.end() && it->second.bytes >= r.bytes ? it->second.d : nullptr;
+  }
+  auto it = g_pcache.find(r.w);
+  if (it == g_pcache.end()) return nullptr;
+  const PEnt& e = it->second;
+  return e.kind == r.kind && e.in_dim == r.in_dim && e.out_dim == r.out_dim && e.n == r.n ? e.d : nullptr;
+}
+
+// Uploads r's mirror, replacing a smaller or differently shaped one (g_wmu
+// held exclusively).  0 or -1.
+int create(const WReq& r) {
+  if (!r.packed) {
+    auto it = g_wcache.find(r.w);
+    if (it != g_wcache.end()) {
+      (void)hipFree(it->second.d);
+      g_wcache.erase(it);
+    }
+    void* d = nullptr;
+    if (check(hipMalloc(&d, (size_t)r.bytes), "weight upload: hipMalloc")) return -1;
+    if (check(hipMemcpy(d, r.w, (size_t)r.bytes, hipMemcpyHostToDevice), "weight upload: hipMemcpy")) {
+      (void)hipFree(d);
+      return -1;
+    }
+    g_wcache[r.w] = {d, r.bytes};
+    return 0;
+  }
+  auto it = g_pcache.find(r.w);
   if (it != g_pcache.end()) {
-    const PEnt& e = it->second;
-    if (e.kind == kind && e.in_dim == in_dim && e.out_dim == out_dim && e.n == n) return e.d;
-    (void)hipFree(e.d);
+    (void)hipFree(it->second.d);
     g_pcache.erase(it);
   }
-  const size_t one = (size_t)need_bytes(kind, in_dim, out_dim);
-  if (n == 1) src_stride = one;
-  const size_t raw = src_stride * (size_t)(n - 1) + one;
-  const size_t pb = kq::packed_bytes(kind, in_dim, out_dim);
+  // Packed on the device from a temporary ggml copy.
+  const size_t one = (size_t)need_bytes(r.kind, r.in_dim, r.out_dim);
+  const size_t stride = r.n == 1 ? one : r.src_stride;
+  const size_t raw = stride * (size_t)(r.n - 1) + one;
+  const size_t pb = kq::packed_bytes(r.kind, r.in_dim, r.out_dim);
   void *tmp = nullptr, *d = nullptr;
   int rc = check(hipMalloc(&tmp, raw), "weight upload: hipMalloc");
-  if (!rc) rc = check(hipMalloc(&d, pb * (size_t)n), "weight upload: hipMalloc packed");
-  if (!rc) rc = check(hipMemcpy(tmp, w, raw, hipMemcpyHostToDevice), "weight upload: hipMemcpy");
-  for (int i = 0; i < n && !rc; ++i)
-    rc = check(kq::launch_pack(kind, (const uint8_t*)tmp + src_stride * i, in_dim, out_dim, (uint8_t*)d + pb * i,
+  if (!rc) rc = check(hipMalloc(&d, pb * (size_t)r.n), "weight upload: hipMalloc packed");
+  if (!rc) rc = check(hipMemcpy(tmp, r.w, raw, hipMemcpyHostToDevice), "weight upload: hipMemcpy");
+  for (int i = 0; i < r.n && !rc; ++i)
+    rc = check(kq::launch_pack(r.kind, (const uint8_t*)tmp + stride * i, r.in_dim, r.out_dim, (uint8_t*)d + pb * i,
                                false, nullptr),
                "weight upload: pack");
   if (!rc) rc = check(hipStreamSynchronize(nullptr), "weight upload: sync");
   if (tmp) (void)hipFree(tmp);
   if (rc) {
     if (d) (void)hipFree(d);
-    return nullptr;
+    return -1;
   }
-  g_pcache[w] = {d, kind, in_dim, out_dim, n};
-  return d;
+  g_pcache[r.w] = {d, r.kind, r.in_dim, r.out_dim, r.n};
+  return 0;
+}
+
+// Sets every r[i].d and returns 0 with `rd` (a deferred shared lock of
+// g_wmu) locked: the mirrors stay valid until the caller releases it.  Missing
+// mirrors are uploaded under the exclusive lock, then looked up again (another
+// thread may free or replace one in between; a few rounds settle it).  -1,
+// with rd unlocked, if an upload fails.
+int acquire(std::shared_lock<std::shared_mutex>& rd, WReq* r, int n) {
+  for (int round = 0; round < 8; ++round) {
+    rd.lock();
+    bool all = true;
+    for (int i = 0; i < n; ++i) all = (r[i].d = lookup(r[i])) != nullptr && all;
+    if (all) return 0;
+    rd.unlock();
+    std::unique_lock<std::shared_mutex> wr(g_wmu);
+    for (int i = 0; i < n; ++i)
+      if (!lookup(r[i]) && create(r[i])) return -1;
+  }
+  report(-EAGAIN, "weight upload: the cache kept changing under concurrent frees");
+  return -1;
 }
 
 // ---- per-thread execution context -------------------------------------------
 
+// Device buffer that only grows, and never frees a buffer it has handed out:
+// a HIP graph captured while an older, smaller buffer was current keeps its
+// pointer, so a later growth must leave that memory valid.  Growth at least
+// doubles, so the superseded buffers together stay smaller than the current
+// one; all of them live until the process ends.
 template <class T>
 struct DevBuf {
   T* p = nullptr;
   size_t n = 0;
-  int ensure(size_t want, const char* what) {
+  std::vector<T*> old;
+  // 0 or -1; *grew says whether p is a new, uninitialised buffer.
+  int ensure(size_t want, const char* what, bool* grew = nullptr) {
+    if (grew) *grew = false;
     if (want <= n) return 0;
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    n = 0;
-    if (check(hipMalloc(&p, want * sizeof(T)), what)) return -1;
-    n = want;
+    const size_t sz = std::max(want, 2 * n);
+    T* q = nullptr;
+    if (check(hipMalloc(&q, sz * sizeof(T)), what)) return -1;
+    if (p) old.push_back(p);
+    p = q;
+    n = sz;
+    if (grew) *grew = true;
     return 0;
   }
 };
@@ -165,6 +236,20 @@ struct HostBuf {
   }
 };
 
+// Bytes of MvWorkspace::mm for every launch matmul_packed may issue for up
+// to `batch` vectors: the 16-vector kernel, and the 64-vector kernel at each
+// padding (16, 32, 64 vectors) a launch of at most min(batch, 64) vectors
+// takes -- a smaller padding can mean a finer column split and so more
+// partial sums.
+size_t mm_work_bytes(int in_dim, int out_dim, int batch) {
+  size_t n = kq::mm16_workspace_bytes(in_dim, out_dim);
+  for (int bp = 16; bp <= 64; bp *= 2) {
+    n = std::max(n, kq::mfma_workspace_bytes(in_dim, out_dim, bp));
+    if (bp >= batch) break;
+  }
+  return n;
+}
+
 // Partial sums and per-tile arrival counters of the packed matvec
 // (kq::launch_matvec_packed).  Counters start zeroed and every launch leaves
 // them zero; launches sharing a workspace must be ordered on one stream.
@@ -175,14 +260,10 @@ struct MvWorkspace {
   int ensure(int in_dim, int out_dim, int batch = 1) {
     const size_t pf = batch > 1 ? kq::multi_workspace_floats(in_dim, out_dim) : kq::packed_workspace_floats(in_dim, out_dim);
     if (part.ensure(std::max<size_t>(pf, 64), "hipMalloc partials")) return -1;
-    if (batch > 1 && mm.ensure(std::max(kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, 64)),
-                                        kq::mm16_workspace_bytes(in_dim, out_dim)),
-                               "hipMalloc mfma"))
-      return -1;
-    const size_t want = kq::packed_counters(out_dim);
-    if (want <= count.n) return 0;
-    if (count.ensure(want, "hipMalloc counters")) return -1;
-    return check(hipMemset(count.p, 0, count.n * sizeof(unsigned)), "hipMemset counters");
+    if (batch > 1 && mm.ensure(mm_work_bytes(in_dim, out_dim, batch), "hipMalloc mfma")) return -1;
+    bool grew = false;
+    if (count.ensure(kq::packed_counters(out_dim), "hipMalloc counters", &grew)) return -1;
+    return grew ? check(hipMemset(count.p, 0, count.n * sizeof(unsigned)), "hipMemset counters") : 0;
   }
 };
 
@@ -198,37 +279,57 @@ constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;
 std::atomic<int> g_mm_engine{0};
-hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
-                         MvWorkspace& ws, hipStream_t st) {
-  if (batch == 1)
-    return kq::launch_matvec_packed(kind, P, in_dim, out_dim, X, Y, ws.part.p, ws.count.p, st);
+
+// The kernel family of a batched product and how many vectors each launch
+// takes: 0 the multi-vector VALU kernel, 1 the 16-vector and 2 the 64-vector
+// MFMA kernel.
+struct MmRoute {
+  int family, step;
+};
+MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   const int eng = g_mm_engine.load(std::memory_order_relaxed);
   const long units = (long)((out_dim + 63) / 64) * (in_dim / 256);
   const bool mm16 = kq::mm16_kind(kind) &&
                     (eng == 3 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS &&
                                   (batch <= 16 || units >= MM16_MIN_UNITS)));
   const bool mm64 = !mm16 && kq::mfma_kind(kind) && (eng == 2 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS));
-  if (mm16 || mm64) {
-    // Q6_K in launches of at most 32 vectors: the 64-vector kernel's Q6_K
-    // variant runs out of registers above 32 (14336x4096: 359 us for 64
-    // vectors in one launch, 82 us per 32).
-    const int step = mm16 ? 16 : kind == kq::Q6_K ? 32 : 64;
-    for (int b0 = 0; b0 < batch; b0 += step) {
-      const int nb = std::min(step, batch - b0);
-      const float* xb = X + (size_t)b0 * in_dim;
-      float* yb = Y + (size_t)b0 * out_dim;
-      const hipError_t e = mm16 ? kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st,
-                                                         batch <= step)
-                                : kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p,
-                                                                ws.count.p, st, batch <= step);
-      if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
-  }
-  for (int b0 = 0; b0 < batch; b0 += MULTI_MAX_BATCH) {
-    const int nb = std::min(MULTI_MAX_BATCH, batch - b0);
-    const hipError_t e = kq::launch_matmul_packed_valu(kind, P, in_dim, out_dim, nb, X + (size_t)b0 * in_dim,
-                                                       Y + (size_t)b0 * out_dim, ws.part.p, ws.count.p, st);
+  // Q6_K in launches of at most 32 vectors: the 64-vector kernel's Q6_K
+  // variant runs out of registers above 32 (14336x4096: 359 us for 64
+  // vectors in one launch, 82 us per 32).
+  if (mm16) return {1, 16};
+  if (mm64) return {2, kind == kq::Q6_K ? 32 : 64};
+  return {0, MULTI_MAX_BATCH};
+}
+
+// The largest MvWorkspace::mm any launch of matmul_packed needs for this
+// product (launches of `step` vectors and a last one of the remainder).
+size_t mm_launch_need(int kind, int in_dim, int out_dim, int batch) {
+  if (batch <= 1) return 0;
+  const MmRoute r = mm_route(kind, in_dim, out_dim, batch);
+  if (r.family == 0) return 0;
+  if (r.family == 1) return kq::mm16_workspace_bytes(in_dim, out_dim);
+  size_t n = kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, r.step));
+  if (batch > r.step && batch % r.step) n = std::max(n, kq::mfma_workspace_bytes(in_dim, out_dim, batch % r.step));
+  return n;
+}
+
+hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
+                         MvWorkspace& ws, hipStream_t st) {
+  if (batch == 1)
+    return kq::launch_matvec_packed(kind, P, in_dim, out_dim, X, Y, ws.part.p, ws.count.p, st);
+  const MmRoute r = mm_route(kind, in_dim, out_dim, batch);
+  for (int b0 = 0; b0 < batch; b0 += r.step) {
+    const int nb = std::min(r.step, batch - b0);
+    const float* xb = X + (size_t)b0 * in_dim;
+    float* yb = Y + (size_t)b0 * out_dim;
+    hipError_t e;
+    if (r.family == 1)
+      e = kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st, batch <= r.step);
+    else if (r.family == 2)
+      e = kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st,
+                                        batch <= r.step);
+    else
+      e = kq::launch_matmul_packed_valu(kind, P, in_dim, out_dim, nb, xb, yb, ws.part.p, ws.count.p, st);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -321,13 +422,14 @@ extern "C" void aspida_gpu_matvec(const void* w, long wbytes, int kind, int in_d
     fill_nan(y, out_dim);
     return;
   }
-  void* dw = packed_weight(w, kind, in_dim, out_dim);
+  std::shared_lock<std::shared_mutex> rd(g_wmu, std::defer_lock);
+  WReq req = packed_req(w, kind, in_dim, out_dim);
   Ctx& c = ctx();
-  int rc = dw ? 0 : -1;
+  int rc = acquire(rd, &req, 1);
   if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim) ? -1 : 0;
   if (!rc)
     rc = run_host(c, x, in_dim, y, out_dim, in_dim, 1, false, [&]() {
-      return kq::launch_matvec_packed(kind, dw, in_dim, out_dim, c.dx.p, c.dy.p, c.ws.part.p, c.ws.count.p, c.st);
+      return kq::launch_matvec_packed(kind, req.d, in_dim, out_dim, c.dx.p, c.dy.p, c.ws.part.p, c.ws.count.p, c.st);
     });
   if (rc) fill_nan(y, out_dim);
 }
@@ -342,12 +444,13 @@ extern "C" void aspida_gpu_matmul(const void* w, long wbytes, int kind, int in_d
   Ctx& c = ctx();
   // Packed HBM mirror (shared with aspida_gpu_matvec): the multi-vector VALU
   // kernel up to 8 vectors at a time, MFMA for larger Q4_K / Q6_K batches.
-  void* dw = packed_weight(w, kind, in_dim, out_dim);
-  int rc = dw ? 0 : -1;
+  std::shared_lock<std::shared_mutex> rd(g_wmu, std::defer_lock);
+  WReq req = packed_req(w, kind, in_dim, out_dim);
+  int rc = acquire(rd, &req, 1);
   if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim, batch) ? -1 : 0;
   if (!rc)
     rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, false, [&]() {
-      return matmul_packed(kind, dw, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.ws, c.st);
+      return matmul_packed(kind, req.d, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.ws, c.st);
     });
   if (rc) fill_nan(y, (long)out_dim * batch);
 }
@@ -359,9 +462,10 @@ extern "C" void aspida_gpu_dense_matvec(const void* w, long wbytes, int in_dim, 
     fill_nan(y, out_dim);
     return;
   }
-  void* dw = weight(w, (long)in_dim * out_dim * 4);
+  std::shared_lock<std::shared_mutex> rd(g_wmu, std::defer_lock);
+  WReq req = ggml_req(w, (long)in_dim * out_dim * 4);
   Ctx& c = ctx();
-  int rc = dw ? 0 : -1;
+  int rc = acquire(rd, &req, 1);
   if (!rc) {
     if (c.init() || c.dx.ensure((size_t)in_dim, "hipMalloc x") || c.dy.ensure((size_t)out_dim, "hipMalloc y") ||
         c.hx.ensure((size_t)in_dim, "pinned x") || c.hy.ensure((size_t)out_dim, "pinned y"))
@@ -370,7 +474,7 @@ extern "C" void aspida_gpu_dense_matvec(const void* w, long wbytes, int in_dim, 
   if (!rc) {
     std::memcpy(c.hx.p, x, (size_t)in_dim * 4);
     rc = check(hipMemcpyAsync(c.dx.p, c.hx.p, (size_t)in_dim * 4, hipMemcpyHostToDevice, c.st), "H2D x");
-    if (!rc) rc = check(kq::launch_dense((const float*)dw, in_dim, out_dim, c.dx.p, c.dy.p, c.st), "dense");
+    if (!rc) rc = check(kq::launch_dense((const float*)req.d, in_dim, out_dim, c.dx.p, c.dy.p, c.st), "dense");
     if (!rc) rc = check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)out_dim * 4, hipMemcpyDeviceToHost, c.st), "D2H");
     if (!rc) rc = check(hipStreamSynchronize(c.st), "sync");
     if (!rc) std::memcpy(y, c.hy.p, (size_t)out_dim * 4);
@@ -378,8 +482,9 @@ extern "C" void aspida_gpu_dense_matvec(const void* w, long wbytes, int in_dim, 
   if (rc) fill_nan(y, out_dim);
 }
 
+// Waits (exclusive lock) for every host-ABI call that holds a mirror of w.
 extern "C" void aspida_gpu_free_weight(const void* w) {
-  std::lock_guard<std::mutex> lk(g_wmu);
+  std::unique_lock<std::shared_mutex> wr(g_wmu);
   auto it = g_wcache.find(w);
   if (it != g_wcache.end()) {
     (void)hipFree(it->second.d);
@@ -426,41 +531,54 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
   }
   Ctx& c = ctx();
   const bool gated = gate_inp_len > 1 && shared_gate_inp;
+  // Per call, one pinned buffer and one copy carry x | top_w | top_idx and,
+  // when gated, the shared gate's input vector.  That vector is not a cached
+  // weight: the Ada host never frees it through aspida_gpu_free_weight
+  // (LLM_MoE.Free, src/llm/llm_moe.adb:74-79), so a mirror keyed by its
+  // address could outlive it.
+  const size_t nstage = (size_t)dim + 2 * top_k + (gated ? (size_t)dim : 0);
+  const size_t stage = (nstage + 63) & ~(size_t)63;
+  auto stage_inputs = [&]() {
+    std::memcpy(c.hx.p, x, (size_t)dim * 4);
+    std::memcpy(c.hx.p + dim, top_w, (size_t)top_k * 4);
+    std::memcpy(c.hx.p + dim + top_k, top_idx, (size_t)top_k * 4);
+    if (gated) std::memcpy(c.hx.p + dim + 2 * top_k, shared_gate_inp, (size_t)dim * 4);
+    return check(hipMemcpyAsync(c.dh.p, c.hx.p, nstage * 4, hipMemcpyHostToDevice, c.st), "H2D");
+  };
+  std::shared_lock<std::shared_mutex> rd(g_wmu, std::defer_lock);
   // Grouped path over packed experts when gate, up and the shared gate/up
   // share one kind and both downs another (the Q4_K_M layouts do).
   if (gate_kind == up_kind && shg_kind == gate_kind && shu_kind == gate_kind && shd_kind == down_kind &&
       kq::moe_grouped_supported(dim, intermed, 1, top_k) && kq::moe_grouped_experts_ok(n_exp)) {
-    kq::MoeGroupedArgs a{};
     // The per-expert stride of the host tensors is bytes / n_exp (gpu_matvec.cu:1702-1703).
-    a.gate = (const uint8_t*)packed_weight(gate_w, gate_kind, dim, intermed, n_exp, (size_t)(gate_bytes / n_exp));
-    a.up = (const uint8_t*)packed_weight(up_w, up_kind, dim, intermed, n_exp, (size_t)(up_bytes / n_exp));
-    a.down = (const uint8_t*)packed_weight(down_w, down_kind, intermed, dim, n_exp, (size_t)(down_bytes / n_exp));
-    a.sh_gate = (const uint8_t*)packed_weight(shg_w, shg_kind, dim, intermed);
-    a.sh_up = (const uint8_t*)packed_weight(shu_w, shu_kind, dim, intermed);
-    a.sh_down = (const uint8_t*)packed_weight(shd_w, shd_kind, intermed, dim);
+    WReq req[6] = {packed_req(gate_w, gate_kind, dim, intermed, n_exp, (size_t)(gate_bytes / n_exp)),
+                   packed_req(up_w, up_kind, dim, intermed, n_exp, (size_t)(up_bytes / n_exp)),
+                   packed_req(down_w, down_kind, intermed, dim, n_exp, (size_t)(down_bytes / n_exp)),
+                   packed_req(shg_w, shg_kind, dim, intermed), packed_req(shu_w, shu_kind, dim, intermed),
+                   packed_req(shd_w, shd_kind, intermed, dim)};
+    int rc = acquire(rd, req, 6);
+    kq::MoeGroupedArgs a{};
+    a.gate = (const uint8_t*)req[0].d;
+    a.up = (const uint8_t*)req[1].d;
+    a.down = (const uint8_t*)req[2].d;
+    a.sh_gate = (const uint8_t*)req[3].d;
+    a.sh_up = (const uint8_t*)req[4].d;
+    a.sh_down = (const uint8_t*)req[5].d;
     a.gu_stride = kq::packed_bytes(gate_kind, dim, intermed);
     a.d_stride = kq::packed_bytes(down_kind, intermed, dim);
     a.T = 1; a.top_k = top_k; a.n_exp = n_exp; a.dim = dim; a.I = intermed;
-    int rc = (a.gate && a.up && a.down && a.sh_gate && a.sh_up && a.sh_down) ? 0 : -1;
-    if (!rc && gated) {
-      a.sgi = (const float*)weight(shared_gate_inp, (long)dim * 4);
-      if (!a.sgi) rc = -1;
-    }
-    // Staging x | top_w | top_idx, then the grouped work on a 256-byte boundary.
-    const size_t stage = ((size_t)dim + 2 * top_k + 63) & ~(size_t)63;
+    // The staged inputs, then the grouped work on a 256-byte boundary.
     const size_t scratch = stage + (kq::moe_grouped_work_bytes(1, dim, intermed, top_k) + 3) / 4;
     if (!rc && (c.init() || c.dy.ensure((size_t)dim, "hipMalloc y") || c.dh.ensure(scratch, "hipMalloc moe scratch") ||
-                c.hx.ensure((size_t)dim + 2 * top_k, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
+                c.hx.ensure(nstage, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
       rc = -1;
     if (!rc) {
-      std::memcpy(c.hx.p, x, (size_t)dim * 4);
-      std::memcpy(c.hx.p + dim, top_w, (size_t)top_k * 4);
-      std::memcpy(c.hx.p + dim + top_k, top_idx, (size_t)top_k * 4);
-      rc = check(hipMemcpyAsync(c.dh.p, c.hx.p, ((size_t)dim + 2 * top_k) * 4, hipMemcpyHostToDevice, c.st), "H2D");
+      rc = stage_inputs();
       if (!rc) {
         a.x = c.dh.p;
         a.top_w = c.dh.p + dim;
         a.idx = (const int*)(c.dh.p + dim + top_k);
+        a.sgi = gated ? c.dh.p + dim + 2 * top_k : nullptr;
         a.y = c.dy.p;
         kq::moe_grouped_bind(a, c.dh.p + stage);
         rc = check(kq::launch_moe_grouped(a, gate_kind, down_kind, c.st), "moe launch");
@@ -472,42 +590,38 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
     if (rc) fill_nan(y, dim);
     return;
   }
-  kq::MoeWeights mw;
   // The per-expert stride is bytes / n_exp (gpu_matvec.cu:1702-1703).
-  mw.gate = (const uint8_t*)weight(gate_w, gate_bytes);
-  mw.up = (const uint8_t*)weight(up_w, up_bytes);
-  mw.down = (const uint8_t*)weight(down_w, down_bytes);
-  mw.sh_gate = (const uint8_t*)weight(shg_w, shg_bytes);
-  mw.sh_up = (const uint8_t*)weight(shu_w, shu_bytes);
-  mw.sh_down = (const uint8_t*)weight(shd_w, shd_bytes);
+  WReq req[6] = {ggml_req(gate_w, gate_bytes), ggml_req(up_w, up_bytes),   ggml_req(down_w, down_bytes),
+                 ggml_req(shg_w, shg_bytes),   ggml_req(shu_w, shu_bytes), ggml_req(shd_w, shd_bytes)};
+  int rc = acquire(rd, req, 6);
+  kq::MoeWeights mw;
+  mw.gate = (const uint8_t*)req[0].d;
+  mw.up = (const uint8_t*)req[1].d;
+  mw.down = (const uint8_t*)req[2].d;
+  mw.sh_gate = (const uint8_t*)req[3].d;
+  mw.sh_up = (const uint8_t*)req[4].d;
+  mw.sh_down = (const uint8_t*)req[5].d;
   mw.gate_stride = gate_bytes / n_exp;
   mw.up_stride = up_bytes / n_exp;
   mw.down_stride = down_bytes / n_exp;
   mw.gate_kind = gate_kind; mw.up_kind = up_kind; mw.down_kind = down_kind;
   mw.sh_gate_kind = shg_kind; mw.sh_up_kind = shu_kind; mw.sh_down_kind = shd_kind;
   mw.dim = dim; mw.intermed = intermed; mw.n_exp = n_exp;
-  int rc = (mw.gate && mw.up && mw.down && mw.sh_gate && mw.sh_up && mw.sh_down) ? 0 : -1;
-  const float* dsgi = nullptr;
-  if (!rc && gated) {
-    dsgi = (const float*)weight(shared_gate_inp, (long)dim * 4);
-    if (!dsgi) rc = -1;
-  }
-  const size_t scratch = kq::moe_scratch_floats(mw, 1, top_k);
-  if (!rc && (c.init() || c.dx.ensure((size_t)dim, "hipMalloc x") || c.dy.ensure((size_t)dim, "hipMalloc y") ||
-              c.dh.ensure(scratch, "hipMalloc moe scratch") || c.hx.ensure((size_t)dim + 2 * top_k, "pinned x") ||
-              c.hy.ensure((size_t)dim, "pinned y") || c.di.ensure((size_t)top_k, "hipMalloc route")))
+  // The per-slot work follows the staged inputs (moe_staging_floats of them
+  // are set aside at the front of the scratch).
+  const size_t front = std::max(stage, kq::moe_staging_floats(dim, 1, top_k));
+  const size_t scratch = front + kq::moe_scratch_floats(mw, 1, top_k) - kq::moe_staging_floats(dim, 1, top_k);
+  if (!rc && (c.init() || c.dy.ensure((size_t)dim, "hipMalloc y") || c.dh.ensure(scratch, "hipMalloc moe scratch") ||
+              c.hx.ensure(nstage, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
     rc = -1;
   if (!rc) {
-    // Stage x | top_w | top_idx together in one pinned buffer and one copy.
-    std::memcpy(c.hx.p, x, (size_t)dim * 4);
-    std::memcpy(c.hx.p + dim, top_w, (size_t)top_k * 4);
-    std::memcpy(c.hx.p + dim + top_k, top_idx, (size_t)top_k * 4);
-    rc = check(hipMemcpyAsync(c.dh.p, c.hx.p, ((size_t)dim + 2 * top_k) * 4, hipMemcpyHostToDevice, c.st), "H2D");
+    rc = stage_inputs();
     if (!rc) {
       const float* dxx = c.dh.p;
       const float* dtw = c.dh.p + dim;
       const int* dti = (const int*)(c.dh.p + dim + top_k);
-      float* work = c.dh.p + kq::moe_staging_floats(dim, 1, top_k);
+      const float* dsgi = gated ? c.dh.p + dim + 2 * top_k : nullptr;
+      float* work = c.dh.p + front;
       rc = check(kq::launch_moe_experts(mw, 1, top_k, dxx, dti, dtw, dsgi, work, c.dy.p, c.st), "moe launch");
     }
     if (!rc) rc = check(hipMemcpyAsync(c.hy.p, c.dy.p, (size_t)dim * 4, hipMemcpyDeviceToHost, c.st), "D2H");
@@ -813,6 +927,15 @@ extern "C" int aspida_kq_chain_workgroups(void* chain) {
 }
 
 extern "C" void aspida_kq_chain_destroy(void* chain) { kq::chain_destroy((kq::Chain*)chain); }
+
+extern "C" int aspida_kq_matmul_workspace(int kind, int in_dim, int out_dim, int batch, long long* allocated,
+                                          long long* needed) {
+  if (!valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || batch <= 0 || !allocated || !needed)
+    return -EINVAL;
+  *allocated = batch > 1 ? (long long)mm_work_bytes(in_dim, out_dim, batch) : 0;
+  *needed = (long long)mm_launch_need(kind, in_dim, out_dim, batch);
+  return 0;
+}
 
 extern "C" int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile) {
   if (waves_per_group < 0 || groups_per_tile < 0) return -EINVAL;

@@ -314,6 +314,9 @@ __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, in
         __hip_atomic_store(&logits[(size_t)(t0 + tt) * n_exp + e], s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  // Last-arrival handoff of the logits, by the rule stated at mv_epilogue
+  // (kq_packed.h): sc1 atomic stores, retired before the arrival is counted;
+  // the last workgroup reads them with sc1 atomic loads after its count.
   __builtin_amdgcn_s_waitcnt(0);  // the logits stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {

@@ -250,12 +250,29 @@ __device__ __forceinline__ float2 staged_dot2(const typename Packed<KIND>::R& rg
 // workgroups (workspace), then y.  `gtile` indexes the workspace and
 // counters (tiles of every segment of a launch), `tile` the rows of y.
 //
-// Cross-workgroup sum: the partials and the counter are device-scope (sc1)
-// atomics, which bypass the per-XCD L2s, so no agent-scope fence -- an L2
-// write-back and invalidate on this chip -- is needed: the wait below retires
-// the partial store before the arrival is counted, and the last arrival reads
-// the partials only after its counter update returned, adding them in
-// ascending order.
+// Cross-workgroup sum ("last arrival"), and why it needs no fence.  Every
+// cross-workgroup handoff in this library (partial sums here and in the
+// small-batch and resident-chain kernels, router logits, MoE slot outputs)
+// follows the same three steps, and rests on the gfx942/gfx950 memory model
+// as LLVM's AMDGPU backend implements it (AMDGPUUsage, "Memory Model GFX942"):
+//  1. The data are written with agent-scope atomic stores.  At agent scope
+//     these are global_store ... sc1: the store is made coherent across the
+//     XCDs' separate L2s (written through to memory-side coherence), unlike
+//     a plain store, which may stay in one XCD's L2.
+//  2. s_waitcnt vmcnt(0): the wave's stores are acknowledged -- for sc1
+//     stores that is after they reached the coherence point -- before it
+//     issues the agent-scope fetch_add that counts its arrival.
+//  3. The workgroup that sees count == ks - 1 reads the data with
+//     agent-scope atomic loads (global_load ... sc1, which do not return a
+//     stale L2 line).  They are issued only after that fetch_add returned
+//     (control dependence through its result), and every other arrival was
+//     counted only after its stores were acknowledged in step 2.
+// An agent-scope release / acquire pair would add what the backend emits for
+// non-atomic data: buffer_wbl2 (write back the whole L2) before the counter
+// update and buffer_inv (invalidate it) after -- about ten times this
+// epilogue's cost in a first version.  Here no non-atomic data cross
+// workgroups, so those are not needed.  The last arrival adds the partials
+// in ascending order and re-arms the counter for the next launch.
 template <int NW>
 __device__ __forceinline__ void mv_epilogue(float acc, int gtile, int tile, int out_rows, float* __restrict__ y,
                                             float* __restrict__ part, unsigned* __restrict__ count) {

@@ -276,6 +276,18 @@ int aspida_gguf_tensor(const aspida_gguf *g, long long i, aspida_gguf_tensor_inf
  * or a negative errno. */
 long long aspida_gguf_read(const aspida_gguf *g, long long i, void *dst, long long cap);
 
+/* ---- test and tuning hooks (no reference counterpart) ----------------------
+ * The aspida_kq_set_* overrides below change process-wide state that every
+ * thread's next launch reads: call them only while no other thread is calling
+ * the library (tests, tuning runs), never from production callers. */
+
+/* Small-batch workspace check, host only (launches nothing): the bytes of
+ * activation split and partial sums the library allocates for a batched
+ * product of this kind, shape and batch (*allocated), and the most any single
+ * launch of that product uses (*needed).  Returns 0 or -EINVAL. */
+int aspida_kq_matmul_workspace(int kind, int in_dim, int out_dim, int batch, long long *allocated,
+                               long long *needed);
+
 /* Split override for the packed kernels (aspida_kq_packed_plan): waves per
  * workgroup (a power of two <= 16) and workgroups per tile, applied to every
  * shape whose in_dim / 256 they divide; 0, 0 restores the built-in choice.

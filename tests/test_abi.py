@@ -152,3 +152,34 @@ def test_chain_rejects_bad_steps(lib):
     assert lib.aspida_kq_chain_run(None, None) < 0
     assert lib.aspida_kq_chain_check(None) < 0
     lib.aspida_kq_chain_destroy(None)
+
+
+def _matmul_ws(lib, kind, in_dim, out_dim, batch):
+    alloc, need = ctypes.c_longlong(), ctypes.c_longlong()
+    assert lib.aspida_kq_matmul_workspace(kind, in_dim, out_dim, batch, ctypes.byref(alloc), ctypes.byref(need)) == 0
+    return alloc.value, need.value
+
+
+def test_matmul_workspace_covers_every_launch(lib):
+    """The small-batch workspace the library allocates for a product holds
+    what each of its launches writes, for every kind, over shapes of the
+    Qwen2 and Llama families and every batch up to 130 (launch paddings of
+    16, 32 and 64 vectors and the Q6_K step of 32 give different column
+    splits).  Host-only query: no GPU work."""
+    shapes = [(8960, 1536), (1536, 8960), (3584, 3584), (3584, 18944), (18944, 3584), (4096, 4096),
+              (4096, 14336), (14336, 4096), (2048, 768), (768, 2048), (256, 64), (8192, 28672), (28672, 8192)]
+    for kind in aa.KINDS:
+        for in_dim, out_dim in shapes:
+            for batch in list(range(2, 70)) + [96, 97, 127, 128, 130]:
+                alloc, need = _matmul_ws(lib, kind, in_dim, out_dim, batch)
+                assert alloc >= need, (aa.KIND_NAMES[kind], in_dim, out_dim, batch, alloc, need)
+
+
+def test_matmul_workspace_advisor_shapes(lib):
+    """The shapes where a 64-row padding undersized the buffer: Q6_K
+    8960->1536 at B=48 and Q4_K/Q6_K 3584x3584 at B=48 and 65."""
+    for kind, in_dim, out_dim, batch in [(aa.Q6_K, 8960, 1536, 48), (aa.Q4_K, 3584, 3584, 48),
+                                         (aa.Q6_K, 3584, 3584, 48), (aa.Q4_K, 3584, 3584, 65),
+                                         (aa.Q6_K, 3584, 3584, 65)]:
+        alloc, need = _matmul_ws(lib, kind, in_dim, out_dim, batch)
+        assert need > 0 and alloc >= need, (kind, in_dim, out_dim, batch, alloc, need)

@@ -44,6 +44,24 @@ def test_matmul_config_batches(kind, batch, gpu):
                         what=f"{aa.KIND_NAMES[kind]} B={batch}")
 
 
+# Shapes whose launches pad the batch to fewer vectors than the whole batch
+# (Q6_K in steps of 32, a tail of 1 or 16): the workspace must hold each
+# launch's finer column split (Qwen2-1.5B down, Qwen2-7B o).
+@pytest.mark.parametrize("case", [(aa.Q6_K, 8960, 1536, 48), (aa.Q4_K, 3584, 3584, 65), (aa.Q6_K, 3584, 3584, 48),
+                                  (aa.Q4_K, 3584, 3584, 48)], ids=lambda c: f"{aa.KIND_NAMES[c[0]]}_{c[1]}to{c[2]}_B{c[3]}")
+def test_matmul_launch_paddings(case, gpu):
+    kind, in_dim, out_dim, batch = case
+    gen = synth.rng(550 + batch + in_dim)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    Y = gpu.matmul(w, kind, in_dim, out_dim, X)
+    gpu.free_weight(w)
+    assert gpu.last_error() == 0
+    want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
+    assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
+                        what=f"{aa.KIND_NAMES[kind]} {in_dim}->{out_dim} B={batch}")
+
+
 @pytest.mark.parametrize("kind", list(aa.KINDS))
 def test_matmul_all_kinds(kind, gpu):
     gen = synth.rng(600 + kind)

@@ -217,6 +217,51 @@ def test_packed_deterministic_and_graph_replay(dev):
         assert_close_scaled(e.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x), what="graph")
 
 
+def test_graph_replay_survives_workspace_growth(dev):
+    """A graph captured on a stream keeps the workspace pointers of that
+    moment; later, larger calls on the same stream grow the stream's
+    workspace (partials, counters, small-batch buffer).  The library keeps
+    the superseded buffers, so replaying the graph afterwards still gives the
+    eager result, bit for bit."""
+    torch = torch_cuda()
+    gen = synth.rng(67)
+    kind, out_a, in_a = aa.Q4_K, 1024, 4096          # split over workgroups: partials and counters
+    wa, xa = synth.weight_np(kind, out_a, in_a, gen), synth.activations_np(in_a, gen)
+    pa = torch.empty(dev.packed_bytes(kind, in_a, out_a), dtype=torch.uint8, device="cuda")
+    dev.pack(kind, to_dev(wa).data_ptr(), in_a, out_a, pa.data_ptr(), stream())
+    dxa, dya = to_dev(xa), torch.empty(out_a, device="cuda")
+    out_b, in_b, batch = 8192, 14336, 48             # larger matvec and a small-batch product
+    wb = synth.weight_np(kind, out_b, in_b, gen)
+    pb = torch.empty(dev.packed_bytes(kind, in_b, out_b), dtype=torch.uint8, device="cuda")
+    dev.pack(kind, to_dev(wb).data_ptr(), in_b, out_b, pb.data_ptr(), stream())
+    dxb = to_dev(synth.activations_np(batch * in_b, gen))
+    dyb = torch.empty(batch * out_b, device="cuda")
+    s = torch.cuda.Stream()
+    sync()
+    with torch.cuda.stream(s):
+        dev.matvec_packed(kind, pa.data_ptr(), in_a, out_a, dxa.data_ptr(), dya.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    eager = dya.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        dev.matvec_packed(kind, pa.data_ptr(), in_a, out_a, dxa.data_ptr(), dya.data_ptr(), s.cuda_stream)
+    with torch.cuda.stream(s):
+        dev.matvec_packed(kind, pb.data_ptr(), in_b, out_b, dxb.data_ptr(), dyb.data_ptr(), s.cuda_stream)
+        dev.matmul_packed(kind, pb.data_ptr(), in_b, out_b, batch, dxb.data_ptr(), dyb.data_ptr(), s.cuda_stream)
+    s.synchronize()
+    for rep in range(3):
+        dya.fill_(float("nan"))
+        sync()
+        with torch.cuda.stream(s):
+            g.replay()
+            if rep == 1:   # eager work on the grown workspace between replays
+                dev.matvec_packed(kind, pb.data_ptr(), in_b, out_b, dxb.data_ptr(), dyb.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        assert torch.equal(eager, dya), f"replay {rep}"
+    want = oracle.qmatvec(kind, wa, in_a, out_a, xa, nthreads=ncpu())
+    assert_close_scaled(eager.cpu().numpy(), want, abs_dot_scale(kind, wa, in_a, out_a, xa), what="graph")
+
+
 PAIR_CASES = [(aa.Q4_K, 5120, aa.Q6_K, 1024, 4096), (aa.Q5_K, 70, aa.Q6_K, 200, 2048), (aa.Q4_K, 64, aa.Q4_K, 3, 768),
               (aa.Q8_0, 130, aa.Q8_0, 64, 1024), (aa.Q6_K, 17, aa.Q6_K, 33, 14336), (aa.Q3_K, 40, aa.Q2_K, 50, 512)]
 
@@ -451,3 +496,37 @@ def test_q8_0_sixteen_wave_column_walk(dev):
     plan = dev.matvec_plan(kind, in_dim, out_dim)
     assert not plan[0] and plan[1] == 16 and plan[3] == 2, plan
     _check_dev(dev, kind, out_dim, in_dim, 8080, "packed", f"Q8_0 {out_dim}x{in_dim} plan={plan}")
+
+
+@pytest.mark.parametrize("kind,out_dim,in_dim", [(aa.Q4_K, 57344, 8192), (aa.Q6_K, 128256, 8192),
+                                                 (aa.Q6_K, 128256, 4096), (aa.Q4_K, 28672, 4096)],
+                         ids=["70b-gate_up", "70b-head", "8b-head", "8b-gate_up"])
+def test_full_size_decode_launches_sampled_rows(kind, out_dim, in_dim, dev):
+    """The decode launches at their full Llama-3 sizes -- 70B gate|up (Q4_K
+    57344x8192, 264 MB) and head (Q6_K 128256x8192, 862 MB), and the 8B ones --
+    weights generated on the device, packed and run by the packed matvec
+    exactly as the benchmark runs them.  A sample of rows (the first and last
+    64-row tiles, and 384 spread over the rest) is compared with the oracle's
+    QMatVec over the same rows' bytes."""
+    torch = torch_cuda()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7000 + out_dim + kind)
+    raw = synth.blocks_torch(kind, out_dim * (in_dim // 256), generator=g)
+    p = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+    dev.pack(kind, raw.data_ptr(), in_dim, out_dim, p.data_ptr(), stream())
+    x = synth.activations_np(in_dim, synth.rng(out_dim + in_dim))
+    dx = to_dev(x)
+    y = torch.full((out_dim,), float("nan"), device="cuda")
+    dev.matvec_packed(kind, p.data_ptr(), in_dim, out_dim, dx.data_ptr(), y.data_ptr(), stream())
+    sync()
+    gen = synth.rng(out_dim * 3 + kind)
+    rows = np.unique(np.concatenate([np.arange(64), np.arange(out_dim - 64, out_dim),
+                                     gen.choice(out_dim, 384, replace=False)]))
+    bpr = (in_dim // 256) * aa.BLOCK_BYTES[kind]
+    idx = torch.from_numpy(rows).cuda()
+    w_rows = raw.view(out_dim, bpr).index_select(0, idx).cpu().numpy().reshape(-1)
+    del raw, p
+    got = y.cpu().numpy()[rows]
+    want = oracle.qmatvec(kind, w_rows, in_dim, rows.size, x, nthreads=ncpu())
+    assert_close_scaled(got, want, abs_dot_scale(kind, w_rows, in_dim, rows.size, x),
+                        what=f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} ({rows.size} sampled rows)")

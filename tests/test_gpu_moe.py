@@ -36,12 +36,72 @@ def _layer(gen, dim, inter, n_exp, gk=aa.Q4_K, uk=aa.Q4_K, dk=aa.Q6_K, sgk=None,
 def _free(gpu, L):
     for k in ("gate", "up", "down", "shg", "shu", "shd"):
         gpu.free_weight(L[k][0])
-    gpu.free_weight(L["sgi"])
 
 
-def _assert_moe(y, want, what):
-    err = np.max(np.abs(y.astype(np.float64) - want))
-    assert err <= MOE_RTOL * np.max(np.abs(want)), f"{what}: max err {err:.3e} vs max|y| {np.max(np.abs(want)):.3e}"
+# Per output: |y_i - want_i| <= MOE_OUT_RTOL * S_i, where S_i bounds how much
+# f32 rounding in any order can move y_i (first-order propagation of a
+# relative dot-product error through SwiGLU and the combine):
+#   S_i = sum_k |w_k| (|D_k| H_k)_i + |g| (|D_sh| H_sh)_i + |g'| (|sgi| |x|) |y_sh,i|
+#   H_k = |h_k| + |silu(a_k)| (|U_k| |x|) + |u_k| |silu'(a_k)| (|G_k| |x|)
+# with a_k = G_k x, u_k = U_k x, h_k = silu(a_k) u_k (float64, oracle decoders).
+# An output whose terms cancel gets the small bound its terms give, not a
+# fraction of max |y|.
+MOE_OUT_RTOL = 5e-5
+
+
+class _Dq:
+    """Dequantized expert matrices (float64), cached per (tensor, expert)."""
+
+    def __init__(self, L, dim, inter, n_exp):
+        self.L, self.dim, self.inter, self.n_exp, self.c = L, dim, inter, n_exp, {}
+
+    def get(self, name, e):
+        key = (name, e)
+        if key not in self.c:
+            arr, kind = self.L[name]
+            n = self.n_exp if name in ("gate", "up", "down") else 1
+            stride = arr.size // n
+            in_dim, out_dim = (self.inter, self.dim) if name in ("down", "shd") else (self.dim, self.inter)
+            self.c[key] = oracle.dequant(kind, arr[e * stride:(e + 1) * stride], in_dim, out_dim).astype(np.float64)
+        return self.c[key]
+
+
+def _silu(a):
+    return a / (1.0 + np.exp(-a))
+
+
+def _moe_scale(dq, x, top_k, idx, tw, sgi):
+    x = x.astype(np.float64)
+    ax = np.abs(x)
+
+    def slot(g_name, u_name, d_name, e):
+        G, U, D = dq.get(g_name, e), dq.get(u_name, e), dq.get(d_name, e)
+        a, u = G @ x, U @ x
+        sig = 1.0 / (1.0 + np.exp(-a))
+        dsilu = np.abs(sig * (1.0 + a * (1.0 - sig)))
+        H = np.abs(_silu(a) * u) + np.abs(_silu(a)) * (np.abs(U) @ ax) + np.abs(u) * dsilu * (np.abs(G) @ ax)
+        return np.abs(D) @ H, D @ (_silu(a) * u)
+
+    S = np.zeros(dq.dim)
+    for k in range(top_k):
+        S += abs(float(tw[k])) * slot("gate", "up", "down", int(idx[k]))[0]
+    sh, ysh = slot("shg", "shu", "shd", 0)
+    if sgi is None:
+        return S + sh
+    z = float(sgi.astype(np.float64) @ x)
+    g = 1.0 / (1.0 + np.exp(-z))
+    return S + g * sh + g * (1.0 - g) * float(np.abs(sgi.astype(np.float64)) @ ax) * np.abs(ysh)
+
+
+def _assert_moe(y, want, what, scale=None):
+    err = np.abs(y.astype(np.float64) - want)
+    assert np.max(err) <= MOE_RTOL * np.max(np.abs(want)), \
+        f"{what}: max err {np.max(err):.3e} vs max|y| {np.max(np.abs(want)):.3e}"
+    if scale is not None:
+        bad = np.nonzero(~(err <= MOE_OUT_RTOL * scale))[0]
+        assert bad.size == 0, (f"{what}: {bad.size} outputs off their own bound; first [{bad[0]}] err "
+                               f"{err[bad[0]]:.3e} bound {MOE_OUT_RTOL * scale[bad[0]]:.3e} "
+                               f"(max err/scale {np.max(err / scale):.3e})")
 
 
 CASES = [
@@ -60,6 +120,7 @@ def test_moe_experts_abi(case):
     dim, inter, n_exp, top_k, kinds, gated = case
     gen = synth.rng(dim + inter + n_exp + top_k + gated)
     L = _layer(gen, dim, inter, n_exp, *kinds)
+    dq = _Dq(L, dim, inter, n_exp)
     for t in range(3):
         x = synth.activations_np(dim, gen)
         logits = oracle.dense_matvec(L["router"], x)
@@ -69,7 +130,34 @@ def test_moe_experts_abi(case):
                             L["shg"], L["shu"], L["shd"], shared_gate_inp=sgi)
         want = oracle.moe_experts(x, dim, top_k, inter, n_exp, idx, tw, L["gate"], L["up"], L["down"],
                                   L["shg"], L["shu"], L["shd"], shared_gate_inp=sgi, nthreads=ncpu())
-        _assert_moe(y, want, f"token {t}")
+        _assert_moe(y, want, f"token {t}", _moe_scale(dq, x, top_k, idx, tw, sgi))
+    _free(gpu, L)
+
+
+@pytest.mark.parametrize("kinds", [(0, 0, 1, 0, 0, 1), (2, 2, 3, 2, 2, 3)], ids=["grouped", "per_slot"])
+def test_moe_shared_gate_input_read_per_call(kinds):
+    """The shared expert's gate input is read from the caller's vector on
+    every call, never from a device copy keyed by its address: the Ada host
+    does not free it through aspida_gpu_free_weight, so after a model reload
+    at the same address a cached copy would be stale.  Here the vector is
+    rewritten in place between calls (same address, never freed)."""
+    torch_cuda()
+    gpu = aa.LLMGpu()
+    dim, inter, n_exp, top_k = 512, 256, 6, 2
+    gen = synth.rng(1888 + kinds[0])
+    L = _layer(gen, dim, inter, n_exp, *kinds)
+    sgi = L["sgi"]
+    x = synth.activations_np(dim, gen)
+    idx, tw = oracle.route(oracle.dense_matvec(L["router"], x), top_k)
+    dq = _Dq(L, dim, inter, n_exp)
+    for rep, fill in enumerate((None, 3.0, -3.0)):
+        if fill is not None:
+            sgi[:] = fill * np.sign(x) / dim   # same buffer, new contents: the gate moves to ~0.95 / ~0.05
+        y = gpu.moe_experts(x, dim, top_k, inter, n_exp, idx, tw, L["gate"], L["up"], L["down"],
+                            L["shg"], L["shu"], L["shd"], shared_gate_inp=sgi)
+        want = oracle.moe_experts(x, dim, top_k, inter, n_exp, idx, tw, L["gate"], L["up"], L["down"],
+                                  L["shg"], L["shu"], L["shd"], shared_gate_inp=sgi, nthreads=ncpu())
+        _assert_moe(y, want, f"call {rep}", _moe_scale(dq, x, top_k, idx, tw, sgi))
     _free(gpu, L)
 
 
@@ -97,9 +185,18 @@ def test_router_selection_matches_oracle(T):
         oi, ow = oracle.route(gl[t], top_k)
         assert gi[t].tolist() == oi.tolist()
         assert np.allclose(gw[t], ow, rtol=1e-5, atol=1e-7)
-        # and from the oracle's logits it agrees unless a near-tie flips
+        # From the oracle's logits the selection may differ only where two
+        # experts are within the logits' measured error of each other: at
+        # every rank where the two selections name different experts, the
+        # oracle's logits of those two differ by at most the sum of their
+        # GPU-vs-oracle logit errors (a near tie that f32 rounding can flip).
         oi2, _ = oracle.route(ol, top_k)
-        assert len(set(oi2.tolist()) ^ set(gi[t].tolist())) <= 2
+        err = np.abs(gl[t].astype(np.float64) - ol)
+        for r, (a, b) in enumerate(zip(gi[t].tolist(), oi2.tolist())):
+            if a != b:
+                gap = abs(float(ol[a]) - float(ol[b]))
+                assert gap <= err[a] + err[b] + 1e-30, \
+                    f"token {t} rank {r}: GPU chose {a}, oracle {b}; logit gap {gap:.3e} > errors {err[a] + err[b]:.3e}"
 
 
 def test_router_ties_lowest_index():
@@ -147,10 +244,11 @@ def test_moe_layer_device_path(T):
                     dS.data_ptr(), work.data_ptr(), y.data_ptr(), stream())
     sync()
     gi, gw, gy = idx.cpu().numpy(), tw.cpu().numpy(), y.cpu().numpy()
+    dq = _Dq(L, dim, inter, n_exp)
     for t in range(T):
         want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, gi[t], gw[t], L["gate"], L["up"], L["down"],
                                   L["shg"], L["shu"], L["shd"], shared_gate_inp=L["sgi"], nthreads=ncpu())
-        _assert_moe(gy[t], want, f"T={T} token {t}")
+        _assert_moe(gy[t], want, f"T={T} token {t}", _moe_scale(dq, X[t], top_k, gi[t], gw[t], L["sgi"]))
 
 
 # ---- grouped experts over packed expert tensors -------------------------------
@@ -222,10 +320,12 @@ def test_moe_experts_packed(case):
     y1, y2 = _run_packed(dev, L, dim, inter, n_exp, top_k, gk, dk, gated, X, idx, tw)
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32)), "grouped MoE not deterministic"
     sgi = L["sgi"] if gated else None
-    for t in range(T):
+    dq = _Dq(L, dim, inter, n_exp)
+    # Every token for small T; an even sample of 40 tokens for the long ones.
+    for t in sorted(set(np.linspace(0, T - 1, min(T, 40)).astype(int).tolist())):
         want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, idx[t], tw[t], L["gate"], L["up"], L["down"],
                                   L["shg"], L["shu"], L["shd"], shared_gate_inp=sgi, nthreads=ncpu())
-        _assert_moe(y1[t], want, f"T={T} token {t}")
+        _assert_moe(y1[t], want, f"T={T} token {t}", _moe_scale(dq, X[t], top_k, idx[t], tw[t], sgi))
 
 
 def test_moe_experts_packed_repeated_expert():
