@@ -63,6 +63,7 @@ def load(path=None):
         "aspida_kq_matvec_plan": (I, [I, I, I, P, P, P]),
         "aspida_kq_unpack_dev": (I, [I, P, I, I, P, P]),
         "aspida_kq_matvec_packed_dev": (I, [I, P, I, I, P, P, P]),
+        "aspida_kq_matvec_packed_noalloc_dev": (I, [I, P, I, I, P, P, P]),
         "aspida_kq_matmul_packed_dev": (I, [I, P, I, I, I, P, P, P]),
         "aspida_kq_matvec2_packed_dev": (I, [I, P, I, P, I, P, I, P, I, P, P]),
         "aspida_kq_matmul_valu_dev": (I, [I, P, I, I, I, P, P, P, P]),

@@ -754,6 +754,94 @@ extern "C" int aspida_kq_matvec_packed_dev(int kind, const void* packed, int in_
                "aspida_kq_matvec_packed_dev");
 }
 
+// ---- allocation-free batch-1 matvec --------------------------------------------
+//
+// aspida_kq_matvec_packed_noalloc_dev runs aspida_kq_matvec_packed_dev's
+// kernels with their workspace in `scratch`, a fixed device array of this
+// library (one copy per GPU, held until the process ends), so a call never
+// allocates: for code under HIP graph capture, tight serving loops and
+// harnesses that forbid hipMalloc.  Layout: per-tile arrival counters, then
+// the cross-workgroup partial sums.
+constexpr size_t NOALLOC_COUNTER_BYTES = (size_t)1 << 20;  // 4096 64-row tiles (262,144 rows)
+constexpr size_t NOALLOC_PART_BYTES = (size_t)5 << 20;     // 1,310,720 partial sums
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_COUNTER_BYTES + NOALLOC_PART_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+// `scratch`'s device address on each GPU (its host-side name is not one).
+struct NoAllocDevice {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+NoAllocDevice g_noalloc[NOALLOC_MAX_DEVICES];
+
+// The current device's copy of `scratch`, looked up once per device with that
+// device current; null (and t_last_error set) on failure.
+void* noalloc_scratch() {
+  int dev = -1;
+  if (check(hipGetDevice(&dev), "aspida_kq_matvec_packed_noalloc_dev: hipGetDevice")) return nullptr;
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    report(-ENODEV, "aspida_kq_matvec_packed_noalloc_dev: device %d beyond the %d supported", dev,
+           NOALLOC_MAX_DEVICES);
+    return nullptr;
+  }
+  NoAllocDevice& d = g_noalloc[dev];
+  std::call_once(d.once, [&d]() {
+    void* p = nullptr;
+    d.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (d.err == hipSuccess) d.ptr = p;
+  });
+  if (d.err != hipSuccess) {
+    check(d.err, "aspida_kq_matvec_packed_noalloc_dev: hipGetSymbolAddress(scratch)");
+    return nullptr;
+  }
+  return d.ptr;
+}
+
+__global__ void fill_u32(unsigned* __restrict__ p, unsigned v, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+}  // namespace
+
+extern "C" int aspida_kq_matvec_packed_noalloc_dev(int kind, const void* packed, int in_dim, int out_dim,
+                                                   const float* x, float* y, void* stream) {
+  const char* fn = "aspida_kq_matvec_packed_noalloc_dev";
+  if (!packed || !x || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 ||
+      ((uintptr_t)x & 15))
+    return -EINVAL;
+  const size_t ncount = kq::packed_counters(out_dim);
+  const size_t npart = kq::packed_workspace_floats(in_dim, out_dim);
+  if (ncount * sizeof(unsigned) > NOALLOC_COUNTER_BYTES || npart * sizeof(float) > NOALLOC_PART_BYTES) {
+    report(-E2BIG, "%s: %d x %d needs %zu counter and %zu partial-sum bytes; the fixed scratch holds %zu and %zu",
+           fn, out_dim, in_dim, ncount * sizeof(unsigned), npart * sizeof(float), NOALLOC_COUNTER_BYTES,
+           NOALLOC_PART_BYTES);
+    return -E2BIG;
+  }
+  uint8_t* base = (uint8_t*)noalloc_scratch();
+  if (!base) return t_last_error ? t_last_error : -1;
+  unsigned* count = (unsigned*)base;
+  float* part = (float*)(base + NOALLOC_COUNTER_BYTES);
+  const hipStream_t st = (hipStream_t)stream;
+  // The arrival counters must be zero when the launch starts.  Every launch
+  // leaves them zero, but the array is shared with every other call on this
+  // GPU, so they are cleared here -- with a kernel, not a memset node, so the
+  // call may be captured into a HIP graph -- whenever the launch splits a
+  // tile over workgroups (the only case that uses them).
+  const bool mfma = kq::matvec_mfma_takes(kind);
+  const kq::PackedPlan p = mfma ? kq::mfma_plan(kind, in_dim, out_dim) : kq::packed_plan(in_dim, out_dim);
+  if (p.ks > 1 && !p.blk16) {
+    const int blocks = (int)std::min<size_t>((ncount + 255) / 256, 1024);
+    hipLaunchKernelGGL(fill_u32, dim3(blocks), dim3(256), 0, st, count, 0u, ncount);
+    if (check(hipGetLastError(), fn)) return t_last_error;
+  }
+  return check(kq::launch_matvec_packed(kind, packed, in_dim, out_dim, x, y, part, count, st), fn);
+}
+
 extern "C" int aspida_kq_matmul_dev(int kind, const void* w, int in_dim, int out_dim, int batch, const float* x,
                                     const float* xq, float* y, void* stream) {
   if (!w || !x || !xq || !y || !valid_kind(kind) || in_dim <= 0 || in_dim % 256 || out_dim <= 0 || batch <= 0)

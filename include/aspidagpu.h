@@ -126,6 +126,21 @@ int aspida_kq_packed_plan(int in_dim, int out_dim, int *waves_per_group, int *gr
 int aspida_kq_matvec_packed_dev(int kind, const void *packed, int in_dim, int out_dim, const float *x,
                                 float *y, void *stream);
 
+/* Allocation-free form of aspida_kq_matvec_packed_dev: same kernels, launch
+ * split and results (bit for bit), but the workspace -- per-tile arrival
+ * counters and cross-workgroup partial sums -- lives in a fixed device array
+ * of this library (6 MiB, one copy per GPU, held until the process ends), so
+ * the call never allocates device memory: no hipMalloc, hipFree or allocating
+ * library routine.  No counterpart in the reference.  For callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Limit: out_dim up to 262,144 rows and at most 1,310,720
+ * partial sums (tiles x workgroups per tile x 64); larger shapes return
+ * -E2BIG and launch nothing.  Every call on one GPU shares the array, so calls
+ * that overlap in time on one GPU (different streams or threads) race and
+ * give wrong results: order them on one stream.  x must be 16-byte aligned. */
+int aspida_kq_matvec_packed_noalloc_dev(int kind, const void *packed, int in_dim, int out_dim, const float *x,
+                                        float *y, void *stream);
+
 /* y_a = A x and y_b = B x for two packed matrices that share the input (e.g.
  * the q|k and v projections of a decoder layer), in one launch for the kind
  * pairs (Q4_K, Q6_K), (Q5_K, Q6_K) and equal kinds Q4_K, Q5_K, Q6_K, Q8_0;
