@@ -245,13 +245,11 @@ __device__ __forceinline__ uint32_t dword_of(const uint4& v, int j) {
 
 // One super-block column of RB row blocks: the A image, the row blocks' MFMA
 // chains interleaved (consecutive MFMAs independent), then the scales.
-template <int RB>
-__device__ __forceinline__ void mv_column(const MvCol<Q4_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q4_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
+template <int RB, int IL>
+__device__ __forceinline__ void mv_dot(const MvCol<Q4_K, RB>& c, const uint4 (&img)[8][IL], const float* xsum,
+                                       float invS, const MvLane& L, MvHdr<Q4_K>* hdr, int lane,
+                                       float (&acc)[RB]) {
   const int g = lane >> 4, n = lane & 15;
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q4_K>(xv, L, xsum);
   if (RB == 4) hdr->h[lane] = c.h;
   __builtin_amdgcn_wave_barrier();
   uint4 A[8];
@@ -291,13 +289,20 @@ __device__ __forceinline__ void mv_column(const MvCol<Q4_K, RB>& c, float4 xv, c
   }
 }
 
-template <int RB>
-__device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q6_K>* hdr, int lane,
+template <int RB, int IL = (RB == 4 ? 64 : 17)>
+__device__ __forceinline__ void mv_column(const MvCol<Q4_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q4_K>* hdr, int lane,
                                           float (&acc)[RB]) {
-  const int g = lane >> 4, n = lane & 15;
   __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q6_K>(xv, L, xsum);
+  const float invS = build_image<Q4_K>(xv, L, xsum);
+  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
+}
+
+template <int RB, int IL>
+__device__ __forceinline__ void mv_dot(const MvCol<Q6_K, RB>& c, const uint4 (&img)[8][IL], const float* xsum,
+                                       float invS, const MvLane& L, MvHdr<Q6_K>* hdr, int lane,
+                                       float (&acc)[RB]) {
+  const int g = lane >> 4, n = lane & 15;
   if (RB == 4) {
     hdr->sc[lane] = c.sc;
     hdr->d[lane] = c.d;
@@ -357,6 +362,15 @@ __device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, c
   }
 }
 
+template <int RB, int IL = (RB == 4 ? 64 : 17)>
+__device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q6_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q6_K>(xv, L, xsum);
+  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
+}
+
 // Q5_K (Decode_Q5K_Block, llm_dequant.adb:426-498): Q4_K's columns with a
 // fifth code bit, code = nibble + 16 hbit.  The nibbles take Q4_K's MFMAs; the
 // fifth bits take one more MFMA each, against the same activation fragments,
@@ -364,13 +378,11 @@ __device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, c
 // in place as the subnormals 2^(2g-24) and 2^(2g+1-24).  Their sums are
 // scaled back per lane: 16 2^-2g for sub-block 2g, and 16 2^-(2g+1) 16 for
 // 2g + 1, whose activations the image holds divided by 16.
-template <int RB>
-__device__ __forceinline__ void mv_column(const MvCol<Q5_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q5_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
+template <int RB, int IL>
+__device__ __forceinline__ void mv_dot(const MvCol<Q5_K, RB>& c, const uint4 (&img)[8][IL], const float* xsum,
+                                       float invS, const MvLane& L, MvHdr<Q5_K>* hdr, int lane,
+                                       float (&acc)[RB]) {
   const int g = lane >> 4, n = lane & 15;
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q5_K>(xv, L, xsum);
   if (RB == 4) hdr->h[lane] = c.h;
   __builtin_amdgcn_wave_barrier();
   uint4 A[8];
@@ -415,19 +427,26 @@ __device__ __forceinline__ void mv_column(const MvCol<Q5_K, RB>& c, float4 xv, c
   }
 }
 
+template <int RB, int IL = (RB == 4 ? 64 : 17)>
+__device__ __forceinline__ void mv_column(const MvCol<Q5_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q5_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q5_K>(xv, L, xsum);
+  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
+}
+
 // Q2_K: element 128 nh + 32 k + 16 g + l is field k of qs byte
 // 32 nh + 16 g + l with scale/min byte 8 nh + 2 k + g (Decode_Q2K_Block,
 // llm_dequant.adb:304-320) -- the element and sub-block layout of Q6_K's
 // quarters, so the A image is Q6_K's.  MFMA (T, j) takes fields 2T, 2T + 1 of
 // qs dword j left in place: code q of field k is the subnormal q 2^(2k-24),
 // whose factor 4^k the scales absorb.
-template <int RB>
-__device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q2_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
+template <int RB, int IL>
+__device__ __forceinline__ void mv_dot(const MvCol<Q2_K, RB>& c, const uint4 (&img)[8][IL], const float* xsum,
+                                       float invS, const MvLane& L, MvHdr<Q2_K>* hdr, int lane,
+                                       float (&acc)[RB]) {
   const int g = lane >> 4, n = lane & 15;
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q2_K>(xv, L, xsum);
   if (RB == 4) {
     hdr->sc[lane] = c.sc;
     hdr->d[lane] = c.d;
@@ -483,6 +502,15 @@ __device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, c
   }
 }
 
+template <int RB, int IL = (RB == 4 ? 64 : 17)>
+__device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q2_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q2_K>(xv, L, xsum);
+  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
+}
+
 // Q3_K (Decode_Q3K_Block, llm_dequant.adb:207-268): Q2_K's element layout
 // with a high bit, code = low2 + 4 hbit, w = d (sc - 32) (code - 4).  Since
 // code - 4 = low2 - 4 (1 - hbit), the low-bit fields take Q2_K's MFMAs and the
@@ -491,13 +519,11 @@ __device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, c
 // back per lane by -4 2^-(4nh+k).  No sum of x is subtracted: a zero weight
 // (code 4) adds nothing to either sum, so a large activation there cannot
 // leave the matrix cores' truncation error of a cancelled term behind.
-template <int RB>
-__device__ __forceinline__ void mv_column(const MvCol<Q3_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<Q3_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
+template <int RB, int IL>
+__device__ __forceinline__ void mv_dot(const MvCol<Q3_K, RB>& c, const uint4 (&img)[8][IL], const float* xsum,
+                                       float invS, const MvLane& L, MvHdr<Q3_K>* hdr, int lane,
+                                       float (&acc)[RB]) {
   const int g = lane >> 4, n = lane & 15, nh = g >> 1, gg = g & 1;
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q3_K>(xv, L, xsum);
   if (RB == 4) {
     hdr->sc[lane] = c.sc;
     hdr->d[lane] = c.d;
@@ -554,6 +580,15 @@ __device__ __forceinline__ void mv_column(const MvCol<Q3_K, RB>& c, float4 xv, c
   }
 }
 
+template <int RB, int IL = (RB == 4 ? 64 : 17)>
+__device__ __forceinline__ void mv_column(const MvCol<Q3_K, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q3_K>* hdr, int lane,
+                                          float (&acc)[RB]) {
+  __builtin_amdgcn_wave_barrier();
+  const float invS = build_image<Q3_K>(xv, L, xsum);
+  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
+}
+
 // The LDS one wave uses: its A image, sub-block sums and row headers.
 template <int KA, int KB>
 struct MvShared {
@@ -588,6 +623,16 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
                                               const float* __restrict__ x, uint4 (&img)[8][RB == 4 ? 64 : 17],
                                               float* xsum, MvHdr<KIND>* hdr, int lane, int rb0 = 0) {
   constexpr int GB = 64 * Block<KIND>::BYTES;
+  const uint8_t* gp = P + ((size_t)tile * nsb + sb0) * GB;
+  const float* xp = x + (size_t)sb0 * 256 + 4 * lane;
+
+  // Each column's activations are requested before its weights: the loads
+  // return in order, so the activation image can be built while the weights
+  // are still on their way.  The first loads go out before anything else.
+  MvCol<KIND, RB> c0;
+  float4 x0;
+  __builtin_memcpy(&x0, __builtin_assume_aligned(xp, 16), 16);
+  c0.load(gp, lane, rb0);
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     if (RB == 4 || lane < 17) img[j][lane] = make_uint4(0u, 0u, 0u, 0u);
@@ -596,21 +641,14 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
   float acc[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.f;
-  const uint8_t* gp = P + ((size_t)tile * nsb + sb0) * GB;
-  const float* xp = x + (size_t)sb0 * 256 + 4 * lane;
-
-  MvCol<KIND, RB> c0;
-  float4 x0;
-  c0.load(gp, lane, rb0);
-  __builtin_memcpy(&x0, __builtin_assume_aligned(xp, 16), 16);
   if (PIPE == MV_ONE) {
     mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
   } else if (PIPE == MV_SEQ) {  // columns one after another: one register set, more waves per CU
     for (int s = 0; s < spw; ++s) {
       if (s > 0) {
         asm volatile("" ::: "memory");  // the next column's loads stay after this column's work
-        c0.load(gp + (size_t)s * GB, lane, rb0);
         __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)s * 256, 16), 16);
+        c0.load(gp + (size_t)s * GB, lane, rb0);
       }
       mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
     }
@@ -621,13 +659,13 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
     float4 x1;
     for (int s = 0; s < spw; s += 2) {
       const int s1 = s + 1 < spw ? s + 1 : s;
-      c1.load(gp + (size_t)s1 * GB, lane, rb0);
       __builtin_memcpy(&x1, __builtin_assume_aligned(xp + (size_t)s1 * 256, 16), 16);
+      c1.load(gp + (size_t)s1 * GB, lane, rb0);
       asm volatile("" ::: "memory");  // keep these loads issued here
       mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
       if (s + 2 < spw) {
-        c0.load(gp + (size_t)(s + 2) * GB, lane, rb0);
         __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)(s + 2) * 256, 16), 16);
+        c0.load(gp + (size_t)(s + 2) * GB, lane, rb0);
         asm volatile("" ::: "memory");
       }
       if (s + 1 < spw) mv_column(c1, x1, L, img, xsum, hdr, lane, acc);

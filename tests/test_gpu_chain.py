@@ -148,17 +148,18 @@ def _decoder_spec(layers):
 
 def test_chain_decoder_layers():
     """Two Llama-3-8B layers (q|k, v, o, gate|up, down), each input the
-    previous output."""
+    previous output, run three times in a row."""
     dev = aa.DeviceOps()
     gen = synth.rng(31337)
     spec = _decoder_spec(2)
     ar, W, keep, ch = _build(dev, spec, gen)
     try:
-        ar.put("x0", synth.activations_np(4096, gen))
-        ch.run(stream())
-        sync()
-        assert ch.check()
-        _check(ar, W, spec, "decoder")
+        for rep in range(3):                     # a new epoch per launch
+            ar.put("x0", synth.activations_np(4096, gen))
+            ch.run(stream())
+            sync()
+            assert ch.check()
+            _check(ar, W, spec, f"decoder run {rep}")
         assert ch.workgroups() >= 16 and ch.workgroups() % 16 == 0
     finally:
         ch.close()
