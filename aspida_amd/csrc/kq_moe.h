@@ -43,6 +43,17 @@ hipError_t launch_moe_experts(const MoeWeights& w, int T, int top_k, const float
 constexpr int MOE_MAX_JOBS = 1024;
 // Routed experts the grouped path schedules (LDS tables per workgroup).
 constexpr int MOE_MAX_EXP = 1024;
+// Bitmask words of the schedule's slot ranks ((n_exp + 1) * ceil(T top_k /
+// 32) of them; more than this and it counts ranks by scanning instead).
+constexpr int MOE_SCHED_MASK_WORDS = 2048;
+// Jobs per chunk of the matrix-core grouped launches (kq_moe_mfma.hip).
+constexpr int MOE_MFMA_JPW = 2;
+
+// Chunks of up to jpw jobs a schedule can produce: T (top_k + 1) jobs over
+// at most `routed` routed experts plus the shared one.
+inline long moe_max_chunks(int T, int top_k, int routed, int jpw) {
+  return ((long)T * (top_k + 1) + jpw - 1) / jpw + routed + 1;
+}
 
 // Packed expert tensors: expert e's matrix at base + e * stride (stride =
 // packed bytes of one [rows][cols] matrix); the shared expert's matrices
@@ -57,13 +68,15 @@ struct MoeGroupedArgs {
   const float* sgi;      // shared gate input [dim] or null
   float *h, *yk, *gsh, *y;
   unsigned* count;       // [T][blocks_dim] arrival counters, one per 256 bytes
+  int* sched;            // the schedule the gate/up launch publishes: joff[n_exp + 2], jobs[T (top_k + 1)]
+  int4* units;           // matrix-core launches: [0].x = chunk count, [1 + c] = chunk c {expert, job, job | -1}
   int T, top_k, n_exp, dim, I;
   int tiles_dim;         // 64-row tiles of dim (vector-ALU down projection)
   int blocks_dim;        // 16-row blocks of dim (matrix-core down projection)
 };
 
 size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k);
-// Points h, yk, gsh, count into `work` (moe_grouped_work_bytes of a.T, a.dim,
+// Points h, yk, gsh, count, sched, units into `work` (moe_grouped_work_bytes of a.T, a.dim,
 // a.I, a.top_k, 256-byte aligned) and sets tiles_dim, blocks_dim.  The counters need no
 // clearing: the gate/up launch zeroes them.
 void moe_grouped_bind(MoeGroupedArgs& a, void* work);
@@ -75,6 +88,10 @@ bool moe_grouped_experts_ok(int n_exp);
 // other kinds -- and every kind under aspida_kq_set_mv_engine(1) -- on the
 // vector ALUs (64-row tiles).
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
+// The grouped launches on the matrix cores (kq_moe_mfma.hip): Q4_K and Q6_K
+// projections, any T; hipErrorNotSupported for other kinds.
+bool moe_mfma_kind(int kind);
+hipError_t launch_moe_grouped_mfma(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
 
 // Router: logits[t] = router_w[n_exp][dim] . x[t] (f32), stable softmax,
 // greedy top-k (strict >, lowest index wins ties), renormalised weights

@@ -29,99 +29,16 @@
 
 #include "kq_kernels.h"
 #include "kq_moe.h"
+#include "kq_moe_sched.h"
 #include "kq_mv_mfma.h"
 #include "kq_packed.h"
 
 namespace kq {
 
 
-// ---- schedule ---------------------------------------------------------------------
-//
-// Work items are (expert, 64-row tile, chunk of up to MOE_JPW jobs), the
-// shared expert being expert n_exp with every token's slot top_k.  Every
-// workgroup derives the same schedule from top_idx in LDS: jobs per expert
-// (LDS atomics: counts do not depend on order), exclusive sums of the
-// per-expert chunk and job counts (one wave), then the jobs bucketed by
-// expert in ascending slot order -- a slot's place is the number of earlier
-// slots routed to the same expert, so all workgroups agree on which jobs form
-// each chunk.  Items are numbered expert-major, then tile, then chunk, so the
-// chunks that share an expert tile are adjacent and run close together in
-// time (their weights are read from HBM about once).
+// The schedule of work items (moe_schedule, moe_item) and the gate/up
+// prologue are in kq_moe_sched.h; these kernels take chunks of MOE_JPW jobs.
 constexpr int MOE_JPW = 4;
-
-struct MoeSched {
-  int idx[MOE_MAX_JOBS];       // top_idx, flat
-  int fill[MOE_MAX_EXP + 1];   // jobs per expert
-  int coff[MOE_MAX_EXP + 2];   // exclusive sum of chunks per expert
-  int joff[MOE_MAX_EXP + 2];   // exclusive sum of jobs per expert
-  int jobs[2 * MOE_MAX_JOBS];  // t * slots + k, bucketed by expert, ascending
-};
-
-// Returns the number of chunks (items per tile).
-__device__ int moe_schedule(const int* __restrict__ idx, int T, int top_k, int n_exp, MoeSched& S) {
-  const int n = T * top_k, ne = n_exp + 1, slots = top_k + 1;
-  const int tid = threadIdx.x, bs = blockDim.x;
-  for (int i = tid; i < ne; i += bs) S.fill[i] = i == n_exp ? T : 0;
-  for (int i = tid; i < n; i += bs) S.idx[i] = idx[i];
-  __syncthreads();
-  for (int i = tid; i < n; i += bs) {
-    const int e = S.idx[i];
-    if (e >= 0 && e < n_exp) atomicAdd(&S.fill[e], 1);
-  }
-  __syncthreads();
-  if (tid < 64) {
-    const int lane = tid;
-    int run_c = 0, run_j = 0;
-    for (int base = 0; base < ne; base += 64) {
-      const int e = base + lane;
-      const int c = e < ne ? S.fill[e] : 0;
-      const int ch = wave_scan_add((c + MOE_JPW - 1) / MOE_JPW), jc = wave_scan_add(c);  // inclusive
-      if (e < ne) {
-        S.coff[e] = run_c + ch - (c + MOE_JPW - 1) / MOE_JPW;
-        S.joff[e] = run_j + jc - c;
-      }
-      run_c += __builtin_amdgcn_readlane(ch, 63);
-      run_j += __builtin_amdgcn_readlane(jc, 63);
-    }
-    if (lane == 0) {
-      S.coff[ne] = run_c;
-      S.joff[ne] = run_j;
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < n; i += bs) {
-    const int e = S.idx[i];
-    if (e >= 0 && e < n_exp) {
-      int rank = 0;
-      for (int q = 0; q < i; ++q) rank += S.idx[q] == e;
-      S.jobs[S.joff[e] + rank] = (i / top_k) * slots + i % top_k;
-    }
-  }
-  for (int t = tid; t < T; t += bs) S.jobs[S.joff[n_exp] + t] = t * slots + top_k;
-  __syncthreads();
-  return S.coff[ne];
-}
-
-struct MoeItem {
-  int e, tile, j0, nj;  // expert, tile, first job (into S.jobs), job count
-};
-
-__device__ __forceinline__ MoeItem moe_item(const MoeSched& S, int ne, int tiles, int i) {
-  int lo = 0, hi = ne - 1;  // the expert e with coff[e] * tiles <= i < coff[e + 1] * tiles
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (S.coff[mid] * tiles <= i) lo = mid;
-    else hi = mid - 1;
-  }
-  const int e = lo, ch = S.coff[e + 1] - S.coff[e], r = i - S.coff[e] * tiles;
-  const int c = r % ch, cnt = S.joff[e + 1] - S.joff[e];
-  MoeItem it;
-  it.e = e;
-  it.tile = r / ch;
-  it.j0 = S.joff[e] + c * MOE_JPW;
-  it.nj = cnt - c * MOE_JPW < MOE_JPW ? cnt - c * MOE_JPW : MOE_JPW;
-  return it;
-}
 
 // ---- kernels ------------------------------------------------------------------------
 //
@@ -136,43 +53,6 @@ constexpr int moe_gu_waves(int kind, int nw) {
   return (kind == Q6_K || kind == Q8_0 || nw < 4) ? 1 : nw / 2;
 }
 
-// Housekeeping for the down launch, done by the gate/up launch: zero its
-// arrival counters (workgroup 0), and the shared-expert gate
-// g_t = sigmoid(shared_gate_inp . x_t) (llm_moe.adb:285-293), one wave per
-// token.
-__device__ __forceinline__ void moe_gu_prologue(const MoeGroupedArgs& a, const float* __restrict__ x, int nw, int w,
-                                                int lane) {
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < a.T * a.blocks_dim; i += blockDim.x) a.count[(size_t)i * COUNTER_STRIDE] = 0u;
-  for (int t = blockIdx.x * nw + w; t < a.T; t += gridDim.x * nw) {
-    float s = 0.f;
-    if (a.sgi) {
-      // dim / 256 float4 per lane, loaded together (dim is a multiple of 256).
-      const float4* g4 = reinterpret_cast<const float4*>(a.sgi) + lane;
-      const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)t * a.dim) + lane;
-      for (int b = 0; b < a.dim / 4; b += 64 * 8) {
-        float4 gv[8], xv[8];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const int i = b + 64 * r < a.dim / 4 ? b + 64 * r : 0;
-          gv[r] = g4[i];
-          xv[r] = x4[i];
-        }
-#pragma unroll
-        for (int r = 0; r < 8; ++r)
-          if (b + 64 * r < a.dim / 4) {
-            s = __builtin_fmaf(gv[r].x, xv[r].x, s);
-            s = __builtin_fmaf(gv[r].y, xv[r].y, s);
-            s = __builtin_fmaf(gv[r].z, xv[r].z, s);
-            s = __builtin_fmaf(gv[r].w, xv[r].w, s);
-          }
-      }
-      s = wave_total(s);
-    }
-    if (lane == 0) a.gsh[t] = a.sgi ? 1.0f / (1.0f + expf(-s)) : 1.0f;
-  }
-}
-
 template <int KIND, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_waves(KIND, NW)))) void moe_gate_up(MoeGroupedArgs a, int cpw, const float* __restrict__ x,
                                                       float* __restrict__ h) {
@@ -183,11 +63,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(moe_gu_
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slots = a.top_k + 1, ne = a.n_exp + 1, tiles = a.I / 64;
   moe_gu_prologue(a, x, NW, w, lane);
-  const int items = moe_schedule(a.idx, a.T, a.top_k, a.n_exp, S) * tiles;
+  const int items = moe_schedule<MOE_JPW>(a, S) * tiles;
   constexpr int GB = 64 * Block<KIND>::BYTES;
   const size_t nsb = (size_t)NW * cpw;
   for (int i = blockIdx.x; i < items; i += gridDim.x) {
-    const MoeItem it = moe_item(S, ne, tiles, i);
+    const MoeItem it = moe_item<MOE_JPW>(S, ne, tiles, i);
     const bool shared = it.e == a.n_exp;
     const uint8_t* G = (shared ? a.sh_gate : a.gate + (size_t)it.e * a.gu_stride) + (size_t)it.tile * nsb * GB;
     const uint8_t* U = (shared ? a.sh_up : a.up + (size_t)it.e * a.gu_stride) + (size_t)it.tile * nsb * GB;
@@ -238,11 +118,11 @@ __global__ __launch_bounds__(64 * NW) void moe_down(MoeGroupedArgs a, int cpw, c
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slots = a.top_k + 1, ne = a.n_exp + 1, tiles = a.tiles_dim;
-  const int items = moe_schedule(a.idx, a.T, a.top_k, a.n_exp, S) * tiles;
+  const int items = moe_schedule_load<MOE_JPW>(a, S) * tiles;
   constexpr int GB = 64 * Block<KIND>::BYTES;
   const size_t nsb = (size_t)NW * cpw;
   for (int i = blockIdx.x; i < items; i += gridDim.x) {
-    const MoeItem it = moe_item(S, ne, tiles, i);
+    const MoeItem it = moe_item<MOE_JPW>(S, ne, tiles, i);
     const bool shared = it.e == a.n_exp;
     const uint8_t* D = (shared ? a.sh_down : a.down + (size_t)it.e * a.d_stride) + (size_t)it.tile * nsb * GB;
     for (int j = 0; j < it.nj; ++j) part[j][w][lane] = 0.f;  // this wave's slots only
@@ -385,6 +265,8 @@ size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k) {
   n += (size_t)T * slots * dim * 4;                           // yk
   n += ((size_t)T * 4 + 255) / 256 * 256;                     // gsh
   n += (size_t)T * ((dim + 15) / 16) * COUNTER_STRIDE * 4;    // counters
+  n += ((MOE_MAX_EXP + 2 + (size_t)T * slots) * 4 + 255) / 256 * 256;  // schedule
+  n += (size_t)(1 + moe_max_chunks(T, top_k, T * top_k, MOE_MFMA_JPW)) * 16;  // chunk table
   return n;
 }
 
@@ -398,6 +280,10 @@ void moe_grouped_bind(MoeGroupedArgs& a, void* work) {
   a.gsh = (float*)p;
   p += ((size_t)a.T * 4 + 255) / 256 * 256;
   a.count = (unsigned*)p;
+  p += (size_t)a.T * ((a.dim + 15) / 16) * COUNTER_STRIDE * 4;
+  a.sched = (int*)p;
+  p += ((MOE_MAX_EXP + 2 + (size_t)a.T * slots) * 4 + 255) / 256 * 256;
+  a.units = (int4*)p;
   a.tiles_dim = (a.dim + 63) / 64;
   a.blocks_dim = (a.dim + 15) / 16;
 }
@@ -532,6 +418,8 @@ hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kin
     if (e != hipSuccess) return e;
     return down_kind == Q4_K ? launch_down1_kind<Q4_K>(a, s) : launch_down1_kind<Q6_K>(a, s);
   }
+  // More tokens: grouped by expert, on the matrix cores for Q4_K / Q6_K.
+  if (mfma_moe(gu_kind) && mfma_moe(down_kind)) return launch_moe_grouped_mfma(a, gu_kind, down_kind, s);
   const hipError_t e = launch_gate_up_valu(a, gu_kind, s);
   if (e != hipSuccess) return e;
   return launch_down_valu(a, down_kind, s);

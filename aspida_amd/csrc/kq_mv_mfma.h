@@ -1,5 +1,5 @@
 // kq_mv_mfma.h -- the column arithmetic of the matrix-core matvec
-// (kq_mv_mfma.hip), shared with the matrix-core MoE experts (kq_moe16.hip):
+// (kq_mv_mfma.hip), shared with the matrix-core MoE experts (kq_moe_mfma.hip):
 // the per-column activation image, the packed column loads of 16-row blocks,
 // and one column's MFMA dot with its scales.  The layout and accuracy notes
 // are at the top of kq_mv_mfma.hip.

@@ -106,8 +106,12 @@ def test_grouped_moe_rejects_bad_arguments(lib):
     pointers are never dereferenced)."""
     assert lib.aspida_moe_packed_work_bytes(0, 2048, 768, 8) < 0
     assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 33) < 0
-    # one token: h 9 x 768, yk 9 x 2048 floats, gsh, 128 counters (16-row blocks of dim) of 256 B
-    assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 8) == 4 * 9 * (768 + 2048) + 256 + 128 * 256
+    # one token: h 9 x 768, yk 9 x 2048 floats, gsh, 128 counters (16-row blocks of dim) of 256 B, the
+    # published schedule (1024 + 2 job offsets and 9 jobs, rounded to 256 B) and the chunk table (a count
+    # and at most ceil(9 / 2) + 8 + 1 chunks of 16 B)
+    sched = ((1024 + 2 + 9) * 4 + 255) // 256 * 256
+    table = (1 + (9 + 1) // 2 + 8 + 1) * 16
+    assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 8) == 4 * 9 * (768 + 2048) + 256 + 128 * 256 + sched + table
     # T * top_k above the per-launch job bound: sized for one chunk of 128 tokens
     assert lib.aspida_moe_packed_work_bytes(1000, 2048, 768, 8) == lib.aspida_moe_packed_work_bytes(128, 2048, 768, 8)
     one = 256
