@@ -241,32 +241,38 @@ struct XTile {
 // Thread t's share of column s's activation tile: x chunks t + 256 u (row
 // i / 64, chunk i % 64: hi 0..31, lo 32..63) and, for t < 4 BP, one chunk of
 // sums (row t / 4: hi 0, 1, lo 2, 3).
+// Register copies of the tile are native vectors: an array of the HIP
+// uint4 class, copied with memcpy, stays in memory (then promoted to LDS,
+// whose per-thread indexing reads the workgroup size from the dispatch
+// packet at every launch).
+typedef uint32_t xu4 __attribute__((ext_vector_type(4)));
+
 template <int MB>
-__device__ __forceinline__ void xtile_load(const MmArgs& a, int s, uint4 (&v)[XTile<MB>::NX], uint4& sv) {
+__device__ __forceinline__ void xtile_load(const MmArgs& a, int s, xu4 (&v)[XTile<MB>::NX], xu4& sv) {
   const int t = threadIdx.x, in_dim = a.nsb * 256;
 #pragma unroll
   for (int u = 0; u < XTile<MB>::NX; ++u) {
     const int i = t + 256 * u, b = i >> 6, part = i & 63;
     const _Float16* src = (part < 32 ? a.xh : a.xl) + (size_t)b * in_dim + (size_t)s * 256 + 8 * (part & 31);
-    v[u] = *reinterpret_cast<const uint4*>(src);
+    v[u] = *reinterpret_cast<const xu4*>(src);
   }
   const int b = (t >> 2) & (XTile<MB>::BP - 1), part = t & 3;  // rows wrap for t >= 4 BP (not stored)
   const _Float16* src = (part < 2 ? a.sh : a.sl) + ((size_t)b * a.nsb + s) * 16 + 8 * (part & 1);
-  sv = *reinterpret_cast<const uint4*>(src);
+  sv = *reinterpret_cast<const xu4*>(src);
 }
 
 template <int MB>
-__device__ __forceinline__ void xtile_store(_Float16* xb, _Float16* sb, const uint4 (&v)[XTile<MB>::NX],
-                                            const uint4& sv) {
+__device__ __forceinline__ void xtile_store(_Float16* xb, _Float16* sb, const xu4 (&v)[XTile<MB>::NX],
+                                            const xu4& sv) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < XTile<MB>::NX; ++u) {
     const int i = t + 256 * u, b = i >> 6, part = i & 63;
-    *reinterpret_cast<uint4*>(xb + b * XROW + (part < 32 ? 0 : 256) + 8 * (part & 31)) = v[u];
+    *reinterpret_cast<xu4*>(xb + b * XROW + (part < 32 ? 0 : 256) + 8 * (part & 31)) = v[u];
   }
   if (t < XTile<MB>::BP * 4) {
     const int b = t >> 2, part = t & 3;
-    *reinterpret_cast<uint4*>(sb + b * SROW + (part < 2 ? 0 : 16) + 8 * (part & 1)) = sv;
+    *reinterpret_cast<xu4*>(sb + b * SROW + (part < 2 ? 0 : 16) + 8 * (part & 1)) = sv;
   }
 }
 
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
   const int s0 = blockIdx.y * a.spw;
   Q4Regs cur, nxt;
-  uint4 xv[XTile<MB>::NX], xsv;
+  xu4 xv[XTile<MB>::NX], xsv;
   load_w(s0, cur);
   xtile_load<MB>(a, s0, xv, xsv);
   xtile_store<MB>(xb[0], sb[0], xv, xsv);
@@ -403,7 +409,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
   const int s0 = blockIdx.y * a.spw;
   Q6Regs cur, nxt;
-  uint4 xv[XTile<MB>::NX], xsv;
+  xu4 xv[XTile<MB>::NX], xsv;
   load_w(s0, cur);
   xtile_load<MB>(a, s0, xv, xsv);
   xtile_store<MB>(xb[0], sb[0], xv, xsv);
