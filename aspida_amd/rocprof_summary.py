@@ -9,6 +9,17 @@ median / min / max duration in microseconds.  Each COUNTER_CSV is a
 ``*_counter_collection.csv`` (``rocprofv3 --pmc ... -f csv``); its counters are
 averaged per kernel symbol and grid.  Output is Markdown.
 
+--segment REGEX N splits the dispatches of every kernel whose symbol matches
+REGEX into N consecutive parts (labelled #1..#N, in dispatch order) -- e.g.
+a table that runs the same kernels at several sizes one after another.
+
+--bench-rows small|kquant (with --traffic) prints one line per row of that
+bench.py table instead: the run's dispatches are cut into rows at each random-
+number kernel (every row draws its input first), a row's dispatches into its
+1 + R ncopy products (bench.py's eager call and R graph replays of ncopy
+weight copies), and each product's kernels get their median duration and
+calibrated HBM bytes beside the row's algorithmic bytes.
+
 With --traffic, the FETCH_SIZE and WRITE_SIZE runs (KiB per dispatch) are
 turned into HBM bytes per launch of each kernel symbol: each counter is scaled
 by what it reads for the probe copy (the __amd_rocclr_copyBuffer dispatch of
@@ -37,17 +48,37 @@ def _col(row, *names):
     raise KeyError(names)
 
 
+SEGMENTS = []  # (regex, parts) from --segment
+
+
+def _segmented(groups):
+    """Split each group whose symbol matches a --segment regex into its parts."""
+    out = {}
+    for key, vals in groups.items():
+        parts = next((n for rx, n in SEGMENTS if re.search(rx, key[0])), 1)
+        if parts > 1 and len(vals) % parts == 0:
+            m = len(vals) // parts
+            for i in range(parts):
+                out[(f"{key[0]} #{i + 1}",) + tuple(key[1:])] = vals[i * m:(i + 1) * m]
+        else:
+            out[key] = vals
+    return out
+
+
 def trace_groups(path, match):
     groups = collections.defaultdict(list)
+    rows = []
     with open(path) as f:
         for r in csv.DictReader(f):
             name = short_name(r["Kernel_Name"])
             if not re.search(match, name):
                 continue
-            grid = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}/{r['Workgroup_Size_X']}"
-            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
-            groups[(name, grid)].append(us)
-    return groups
+            rows.append((int(r["Start_Timestamp"]), name, r))
+    for _, name, r in sorted(rows, key=lambda t: t[0]):
+        grid = f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}/{r['Workgroup_Size_X']}"
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        groups[(name, grid)].append(us)
+    return _segmented(groups)
 
 
 def counter_groups(path, match):
@@ -60,7 +91,7 @@ def counter_groups(path, match):
             grid = _col(r, "Grid_Size", "Grid_Size_X")
             wg = _col(r, "Workgroup_Size", "Workgroup_Size_X")
             groups[(name, f"{grid}/{wg}", r["Counter_Name"])].append(float(r["Counter_Value"]))
-    return groups
+    return _segmented(groups)
 
 
 def _symbol_means(path, counter, match):
@@ -76,8 +107,8 @@ def _symbol_means(path, counter, match):
             if "copyBuffer" in name:
                 probe = v if probe is None else max(probe, v)
             elif re.search(match, name):
-                vals[name].append(v)
-    return {k: (statistics.fmean(v), len(v)) for k, v in vals.items()}, probe
+                vals[(name,)].append(v)
+    return {k[0]: (statistics.fmean(v), len(v)) for k, v in _segmented(vals).items()}, probe
 
 
 def traffic(fetch_csv, write_csv, probe_kib, match):
@@ -97,6 +128,77 @@ def traffic(fetch_csv, write_csv, probe_kib, match):
     return out
 
 
+# The rows of bench.py's small_batch_table and kquant_table, in run order:
+# (kind name, out_dim, in_dim, batch).
+_KQ = ("Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K")
+BENCH_ROWS = {
+    "small": [(k, o, i, b) for k in ("Q4_K", "Q6_K") for o, i in ((4096, 4096), (14336, 4096))
+              for b in (2, 4, 8, 16, 32, 64)],
+    "kquant": [(k, o, i, 1) for k in _KQ for o, i in ((14336, 4096), (4096, 14336))] + [("Q4_K", 4096, 4096, 1)],
+}
+# Graph replays of each row (one untimed, then the timed ones).
+BENCH_REPLAYS = {"small": 4, "kquant": 5}
+_BLOCK = {"Q4_K": 144, "Q6_K": 210, "Q5_K": 176, "Q3_K": 110, "Q2_K": 84}
+
+
+def _row_dispatches(path, counter=None):
+    """The library's dispatches (kq_*, but not the packing) of each table row,
+    rows cut at every random-number kernel; rows with none are dropped."""
+    recs = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if counter is not None and r["Counter_Name"] != counter:
+                continue
+            recs.append(r)
+    order = "Dispatch_Id" if counter is not None else "Start_Timestamp"
+    recs.sort(key=lambda r: int(r[order]))
+    rows, cur = [], None
+    for r in recs:
+        if "distribution" in r["Kernel_Name"]:
+            cur = []
+            rows.append(cur)
+            continue
+        name = short_name(r["Kernel_Name"])
+        if cur is None or not name.startswith("kq_") or name.startswith("kq_pack"):
+            continue
+        v = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0 if counter is None else \
+            float(r["Counter_Value"])
+        cur.append((name, v))
+    return [r for r in rows if r]
+
+
+def bench_rows(table, trace_csv, fetch_csv, write_csv, probe_kib):
+    t = traffic(fetch_csv, write_csv, probe_kib, r"^kq_")
+    fs, ws = t["fetch_scale"], t["write_scale"]
+    tr, fe, wr = _row_dispatches(trace_csv), _row_dispatches(fetch_csv, "FETCH_SIZE"), \
+        _row_dispatches(write_csv, "WRITE_SIZE")
+    spec = BENCH_ROWS[table]
+    if not len(tr) == len(fe) == len(wr) == len(spec):
+        raise SystemExit(f"rows found: trace {len(tr)}, fetch {len(fe)}, write {len(wr)}; expected {len(spec)}")
+    print(f"Per row ({t['calibration']}; scales {fs}, {ws}); duration = sum of the product's kernels' "
+          "median durations; algorithmic bytes = weights + 4 B (in + out):")
+    print()
+    print("| row | kernels of one product, median µs each | µs | algorithmic bytes | GB/s | HBM bytes "
+          "per product | HBM / weights |")
+    print("|---|---|---|---|---|---|---|")
+    for (kind, o, i, b), rt, rf, rw in zip(spec, tr, fe, wr):
+        wbytes = _BLOCK[kind] * o * (i // 256)
+        ncopy = max(8, -(-int(1.1 * (1 << 30)) // wbytes))
+        calls = 1 + BENCH_REPLAYS[table] * ncopy
+        k = len(rt) // calls
+        if k * calls != len(rt) or len(rf) != len(rt) or len(rw) != len(rt):
+            raise SystemExit(f"{kind} {o}x{i} B={b}: {len(rt)} dispatches for {calls} products")
+        names = [rt[j][0] for j in range(k)]
+        med = [statistics.median(rt[c * k + j][1] for c in range(1, calls)) for j in range(k)]
+        hbm = 1024 * sum(statistics.fmean(rf[c * k + j][1] for c in range(1, calls)) * fs +
+                         statistics.fmean(rw[c * k + j][1] for c in range(1, calls)) * ws for j in range(k))
+        alg = wbytes + 4 * b * (i + o)
+        us = sum(med)
+        label = f"{kind} {o}x{i}" + (f" B={b}" if table == "small" else "")
+        print(f"| {label} | {' + '.join(f'{n} {m:.2f}' for n, m in zip(names, med))} | {us:.2f} | {alg} | "
+              f"{alg / us / 1e3:.0f} | {int(hbm)} | {hbm / wbytes:.3f} |")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("trace")
@@ -105,7 +207,15 @@ def main():
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--probe-kib", type=float, default=262144.0)
     ap.add_argument("--traffic-json")
+    ap.add_argument("--segment", nargs=2, action="append", default=[], metavar=("REGEX", "N"))
+    ap.add_argument("--bench-rows", choices=sorted(BENCH_ROWS))
     args = ap.parse_args()
+    SEGMENTS.extend((rx, int(n)) for rx, n in args.segment)
+    if args.bench_rows:
+        if not args.traffic:
+            raise SystemExit("--bench-rows needs --traffic")
+        bench_rows(args.bench_rows, args.trace, args.traffic[0], args.traffic[1], args.probe_kib)
+        return
     if args.traffic:
         t = traffic(args.traffic[0], args.traffic[1], args.probe_kib, args.match)
         if args.traffic_json:

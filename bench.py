@@ -24,7 +24,9 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -438,6 +440,64 @@ def moe_table(torch, aa, synth, seed, stream):
     return table
 
 
+def abi_path(aa, synth, seed, tokens=4):
+    """The drop-in ABI as the reference's callers use it (LLM_GPU over
+    aspida_gpu_matvec, gpu_matvec.cu:508-529): host x in, host y out, so each
+    call pays its H2D of x, the kernel and its D2H of y.  Per K-quant at the
+    two FFN shapes (median of repeated calls after the first, which mirrors
+    the weight into HBM), and the 8B decode token as 32 x 7 calls plus the
+    head over distinct host weights (4.9 GB, mirrored on the first token)."""
+    import numpy as np
+    gpu = aa.LLMGpu()
+    gen = synth.rng(seed + 7)
+    per_kind = {}
+    for kind in (aa.Q2_K, aa.Q3_K, aa.Q4_K, aa.Q5_K, aa.Q6_K):
+        for out, inp in ((14336, 4096), (4096, 14336)):
+            w = synth.weight_np(kind, out, inp, gen)
+            x = synth.activations_np(inp, gen)
+            gpu.matvec(w, kind, inp, out, x)
+            ts = []
+            for _ in range(30):
+                t0 = time.perf_counter()
+                gpu.matvec(w, kind, inp, out, x)
+                ts.append(time.perf_counter() - t0)
+            assert gpu.last_error() == 0
+            gpu.free_weight(w)
+            t = statistics.median(ts)
+            gbs = aa.weight_bytes(kind, inp, out) / t / 1e9
+            per_kind[f"{aa.KIND_NAMES[kind]} {out}x{inp}"] = {"us": round(t * 1e6, 2), "weight_GBps": round(gbs, 1)}
+    # The reference's seven calls per layer (q, k, v, o, gate, up, down).
+    plan = [(Q4_K, HIDDEN, HIDDEN), (Q4_K, KV, HIDDEN), (Q6_K, KV, HIDDEN), (Q4_K, HIDDEN, HIDDEN),
+            (Q4_K, FFN, HIDDEN), (Q4_K, FFN, HIDDEN), (Q6_K, HIDDEN, FFN)]
+    layers = [[synth.weight_np(kind, out, inp, gen) for kind, out, inp in plan] for _ in range(LAYERS)]
+    head = synth.weight_np(Q6_K, VOCAB, HIDDEN, gen)
+    xs = {HIDDEN: synth.activations_np(HIDDEN, gen), FFN: synth.activations_np(FFN, gen)}
+
+    def token():
+        for ws in layers:
+            for (kind, out, inp), w in zip(plan, ws):
+                gpu.matvec(w, kind, inp, out, xs[inp])
+        gpu.matvec(head, Q6_K, HIDDEN, VOCAB, xs[HIDDEN])
+
+    token()                                          # mirrors every weight into HBM
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        token()
+    t_tok = (time.perf_counter() - t0) / tokens
+    assert gpu.last_error() == 0
+    for ws in layers:
+        for w in ws:
+            gpu.free_weight(w)
+    gpu.free_weight(head)
+    calls = LAYERS * len(plan) + 1
+    print(f"# ABI path (host x/y per call): 8B decode {1 / t_tok:.1f} tok/s, {calls} calls/token", file=sys.stderr,
+          flush=True)
+    return {"decode_8b": {"tok_s": round(1 / t_tok, 2), "ms_per_token": round(t_tok * 1e3, 3),
+                          "calls_per_token": calls, "tokens": tokens},
+            "kquant_matvec": per_kind,
+            "note": "aspida_gpu_matvec with host buffers: per call H2D x, kernel, D2H y, synchronous"}
+
+
 def cpu_baseline(seed, threads):
     """Aspida's CPU QMatVec (restated in C, pooled rows as LLM_Pool does) on the
     same decode stream, timed on a bounded sample: one layer's seven matvecs
@@ -490,6 +550,50 @@ def _cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def host_cpus():
+    """The host's CPUs as lscpu reports them, the CPUs this process may run on,
+    and os.cpu_count()."""
+    info = {"nproc": os.cpu_count(), "allowed": len(os.sched_getaffinity(0)), "model": _cpu_model()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        keys = {"Model name": "model", "CPU(s)": "cpus", "Socket(s)": "sockets", "Core(s) per socket":
+                "cores_per_socket", "Thread(s) per core": "threads_per_core", "CPU max MHz": "max_mhz"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keys:
+                info[keys[k.strip()]] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
+def native_oracle():
+    """The oracle built -march=native for this host, at run time, into a
+    temporary directory (the committed build is -march=x86-64-v3); None when
+    no compiler is at hand."""
+    src = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "kq_oracle.c")
+    out = os.path.join(tempfile.mkdtemp(prefix="oracle_native_"), "liboracle.so")
+    cmd = ["gcc", "-O3", "-march=native", "-ffp-contract=off", "-fPIC", "-std=c11", "-shared", src, "-o", out,
+           "-lm", "-lpthread"]
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return out if r.returncode == 0 else None
+
+
+def copy_probe(torch, mib):
+    """One device-to-device copy of `mib` MiB: the known-size dispatch that
+    calibrates FETCH_SIZE and WRITE_SIZE (aspida_amd.rocprof_summary
+    --traffic --probe-kib)."""
+    a = torch.empty(mib << 20, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
 
 
 def timed_graph(torch, stream, step_fn, steps, warmup):
@@ -559,6 +663,8 @@ def main():
                                                    args.warmup)}), flush=True)
         return
     if args.only:
+        if args.copy_probe_mib:
+            copy_probe(torch, args.copy_probe_mib)
         fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
         return
@@ -594,12 +700,7 @@ def main():
                 "bytes_per_launch": dom["bytes"] // dom["launches"]}
     stream_bytes = 4_875_853_824
     if args.copy_probe_mib:
-        a = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device="cuda")
-        b = torch.empty_like(a)
-        torch.cuda.synchronize()
-        b.copy_(a)
-        torch.cuda.synchronize()
-        del a, b
+        copy_probe(torch, args.copy_probe_mib)
     table = None if args.no_table else kquant_table(torch, aa, synth, args.seed, stream)
     small = None if args.no_table else small_batch_table(torch, aa, synth, args.seed, stream)
     moe = None if args.no_table else moe_table(torch, aa, synth, args.seed, stream)
@@ -608,10 +709,28 @@ def main():
     big = None if args.no_70b else decode_70b(torch, aa, synth, args.seed, stream, args.mv_engine, args.steps,
                                               args.warmup)
 
+    abi = None if args.no_table else abi_path(aa, synth, args.seed)
+
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        cpu = cpu_baseline(args.seed, threads)
+        # This pool gives each GPU a share of 16 host CPUs; worker pools stay
+        # within it whatever the node's CPU count (recorded in "host").
+        host = host_cpus()
+        threads = args.cpu_threads or min(16, host["allowed"] or 1)
+        import oracle
+        base = cpu_baseline(args.seed, threads)
+        builds = {"x86-64-v3": base["value"]}
+        native = native_oracle()
+        if native:
+            oracle.use_library(native)
+            nat = cpu_baseline(args.seed, threads)
+            builds["native"] = nat["value"]
+            if nat["value"] > base["value"]:
+                base = nat
+                base["sample"] += "; oracle built -march=native on this host at run time"
+        cpu = {**base, "builds": builds, "host": host}
+        print(f"# CPU baseline: {builds} tok/s on {threads} threads of {host.get('cpus', host['nproc'])} "
+              f"({host.get('model', host['model'])})", file=sys.stderr, flush=True)
 
     line = {
         "metric": "Llama-3-8B Q4_K_M decode weight stream tok/s (batch 1) + K-quant matvec HBM GB/s",
@@ -625,6 +744,7 @@ def main():
         "gpu_event_ms_per_step": round(gpu_s * 1e3 / args.steps, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "abi_path": abi,
         "kernels": groups,
         "resident_chain": chain_info,
         "kquant_matvec": table,

@@ -51,6 +51,14 @@ def lib():
     return _lib
 
 
+def use_library(path):
+    """Bind a different build of the same oracle source (e.g. one compiled
+    -march=native for the host at run time); later calls use it."""
+    global LIB_PATH, _lib
+    LIB_PATH = path
+    _lib = None
+
+
 def _ptr(a):
     return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
 
