@@ -271,10 +271,10 @@ struct MvWorkspace {
 // Otherwise, by g_mm_engine: 0 picks, 1 forces the multi-vector VALU kernel,
 // 2 the 64-vector and 3 the 16-vector MFMA kernel where the kind has one.
 // The pick (measured on MI355X, Q4_K and Q6_K): up to 4 vectors on VALU;
-// 5-16 on the 16-vector kernel; beyond 16 the 16-vector kernel in launches
-// of 16 when the matrix has at least MM16_MIN_UNITS (64-row tile,
-// super-block column) pairs to spread, else the 64-vector kernel, which then
-// takes the batch in fewer launches (Q6_K: launches of up to 32).
+// 5-16 on the 16-vector kernel; beyond 16 the 64-vector kernel (one launch
+// for Q4_K; Q6_K launches of up to 32), except Q6_K on a matrix with at
+// least MM16_MIN_UNITS (64-row tile, super-block column) pairs, which runs
+// the 16-vector kernel in launches of 16.
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;
@@ -289,9 +289,13 @@ struct MmRoute {
 MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   const int eng = g_mm_engine.load(std::memory_order_relaxed);
   const long units = (long)((out_dim + 63) / 64) * (in_dim / 256);
+  // Q4_K above 16 vectors: one pass of the 64-vector kernel rather than 16
+  // vectors per launch (14336x4096: 32 vectors 37 -> 31 us, 64 vectors
+  // 69 -> 46 us).  Q6_K keeps the 16-vector launches on big matrices (the
+  // 64-vector Q6_K kernel measured equal or slower there).
   const bool mm16 = kq::mm16_kind(kind) &&
                     (eng == 3 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS &&
-                                  (batch <= 16 || units >= MM16_MIN_UNITS)));
+                                  (batch <= 16 || (units >= MM16_MIN_UNITS && kind != kq::Q4_K))));
   const bool mm64 = !mm16 && kq::mfma_kind(kind) && (eng == 2 || (eng == 0 && batch > MULTI_MAX_BATCH_MFMA_KINDS));
   // Q6_K in launches of at most 32 vectors: the 64-vector kernel's Q6_K
   // variant runs out of registers above 32 (14336x4096: 359 us for 64

@@ -149,48 +149,53 @@ struct MmArgs {
                       // Q6_K measured slower with the per-load choice, 29.6 -> 30.1 us)
 };
 
-// Workgroup = 4 waves over one 64-row tile and a range of spw super-block
-// columns; wave w owns weight rows 64 tile + 16 w + (lane % 16).  acc[mb][r]
-// holds activation row 16 mb + 4 (lane / 16) + r of that weight row.  With
+// Workgroup = 4 waves over 64 RB rows (RB tiles) and a range of spw
+// super-block columns; wave w owns weight rows 64 RB tile + 16 (RB w + rb) +
+// (lane % 16), rb < RB.  acc[rb][mb][r] holds activation row 16 mb +
+// 4 (lane / 16) + r of that weight row.  With
 // ks = gridDim.y > 1 column groups per tile, every workgroup stores its
 // 64 x BP partial tile (device-scope stores) and the last to arrive adds the
 // ks partials of each output in ascending order, all 256 threads with every
 // load in flight at once (the host keeps ks <= 256 / BP).
-template <int MB>
-__device__ __forceinline__ void mm_epilogue(const MmArgs& a, f4 (&acc)[MB]) {
+template <int MB, int RB = 1>
+__device__ __forceinline__ void mm_epilogue(const MmArgs& a, f4 (&acc)[RB][MB]) {
   __shared__ unsigned is_last;
-  constexpr int BP = 16 * MB;
-  constexpr int KS_MAX = 256 / BP;
-  constexpr int PER = BP * 64 / 256;  // outputs per thread in the final sum
+  constexpr int BP = 16 * MB, ROWS = 64 * RB;
+  constexpr int PER = BP * ROWS / 256;  // outputs per thread in the final sum
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, j = lane & 15, Q = lane >> 4;
   const int tile = blockIdx.x, ks = gridDim.y;
   const size_t ntiles = gridDim.x;
-  const int rl = 16 * w + j;  // row within the tile
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     f4 sc;
     __builtin_memcpy(&sc, a.inv + 16 * mb + 4 * Q, 16);
-    acc[mb] *= sc;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb][mb] *= sc;
   }
   if (ks == 1) {
-    const int row = 64 * tile + rl;
-    if (row < a.out_dim)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = ROWS * tile + 16 * (RB * w + rb) + j;
+      if (row < a.out_dim)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int b = 16 * mb + 4 * Q + r;
-          if (b < a.B) a.Y[(size_t)b * a.out_dim + row] = acc[mb][r];
-        }
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int b = 16 * mb + 4 * Q + r;
+            if (b < a.B) a.Y[(size_t)b * a.out_dim + row] = acc[rb][mb][r];
+          }
+    }
     return;
   }
-  float* mine = a.part + ((size_t)blockIdx.y * ntiles + tile) * BP * 64;
+  float* mine = a.part + ((size_t)blockIdx.y * ntiles + tile) * BP * ROWS;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __hip_atomic_store(&mine[(16 * mb + 4 * Q + r) * 64 + rl], acc[mb][r], __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __hip_atomic_store(&mine[(16 * mb + 4 * Q + r) * ROWS + 16 * (RB * w + rb) + j], acc[rb][mb][r],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
@@ -200,24 +205,27 @@ __device__ __forceinline__ void mm_epilogue(const MmArgs& a, f4 (&acc)[MB]) {
                   : 0u;
   __syncthreads();
   if (!is_last) return;
-  // Output o = b * 64 + row-in-tile; thread t sums outputs t + 256 i.
+  // Output o = b * ROWS + row-in-block; thread t sums outputs t + 256 i over
+  // the ks partials in ascending order, a partial's PER loads in flight together.
   const int t = threadIdx.x;
-  float v[PER][KS_MAX];
+  float sum[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i)
+    sum[i] = __hip_atomic_load(a.part + (size_t)tile * BP * ROWS + t + 256 * i, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+  for (int k = 1; k < ks; ++k) {
+    float v[PER];
 #pragma unroll
-    for (int k = 0; k < KS_MAX; ++k)
-      v[i][k] = k < ks ? __hip_atomic_load(a.part + ((size_t)k * ntiles + tile) * BP * 64 + t + 256 * i,
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : 0.f;
+    for (int i = 0; i < PER; ++i)
+      v[i] = __hip_atomic_load(a.part + ((size_t)k * ntiles + tile) * BP * ROWS + t + 256 * i, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) sum[i] += v[i];
+  }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    float sum = v[i][0];
-#pragma unroll
-    for (int k = 1; k < KS_MAX; ++k)
-      if (k < ks) sum += v[i][k];
-    const int o = t + 256 * i, b = o >> 6, row = 64 * tile + (o & 63);
-    if (b < a.B && row < a.out_dim) a.Y[(size_t)b * a.out_dim + row] = sum;
+    const int o = t + 256 * i, b = o / ROWS, row = ROWS * tile + o % ROWS;
+    if (b < a.B && row < a.out_dim) a.Y[(size_t)b * a.out_dim + row] = sum[i];
   }
   if (t == 0) __hip_atomic_store(&a.count[(size_t)tile * COUNTER_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -293,29 +301,38 @@ struct Q4Regs {
   uint2 wc[4];
 };
 
-template <int MB, int NB>
+// RB 16-row blocks per wave: the workgroup covers 64 RB rows (RB tiles), so
+// each staged activation tile serves RB times the rows, and each activation
+// fragment read from LDS feeds RB matrix-core products.
+template <int MB, int NB, int RB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void kq_mm_mfma_q4k(MmArgs a) {
   constexpr int GB = 64 * 144, BP = 16 * MB;
   __shared__ __attribute__((aligned(16))) _Float16 xb[NB][BP * XROW];
   __shared__ __attribute__((aligned(16))) _Float16 sb[NB][BP * SROW];
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row = 16 * w + j;  // weight row within the tile
-  const int tile = blockIdx.x;
-  auto load_w = [&](int s, Q4Regs& r) {
-    const uint8_t* g = a.P + ((size_t)tile * a.nsb + s) * GB;
-    r.h = a.nt ? ld16nt(g + 16 * row) : ld16(g + 16 * row);
+  // Row block RB w + rb of the workgroup: tile (4 RB bx + RB w + rb) / 4, rows
+  // 16 ((RB w + rb) % 4) + (lane % 16) of it.
+  auto load_w = [&](int s, Q4Regs (&r)[RB]) {
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) {
-      const uint8_t* src = g + (1 + 2 * gq + (q >> 1)) * 1024 + 16 * row + 8 * (q & 1);
-      r.wc[gq] = a.nt ? ld8nt(src) : ld8(src);
+    for (int rb = 0; rb < RB; ++rb) {
+      const int G = 4 * RB * blockIdx.x + RB * w + rb, row = 16 * (G & 3) + j;
+      const uint8_t* g = a.P + ((size_t)(G >> 2) * a.nsb + s) * GB;
+      r[rb].h = a.nt ? ld16nt(g + 16 * row) : ld16(g + 16 * row);
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const uint8_t* src = g + (1 + 2 * gq + (q >> 1)) * 1024 + 16 * row + 8 * (q & 1);
+        r[rb].wc[gq] = a.nt ? ld8nt(src) : ld8(src);
+      }
     }
   };
-  f4 acc[MB];
+  f4 acc[RB][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = f4{0.f, 0.f, 0.f, 0.f};
   const int s0 = blockIdx.y * a.spw;
-  Q4Regs cur, nxt;
+  Q4Regs cur[RB], nxt[RB];
   xu4 xv[XTile<MB>::NX], xsv;
   load_w(s0, cur);
   xtile_load<MB>(a, s0, xv, xsv);
@@ -328,49 +345,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       load_w(s0 + c + 1, nxt);
       xtile_load<MB>(a, s0 + c + 1, xv, xsv);
     }
-    // d * sc_t in units of the code placement, dmin, and the eight mins as an
-    // f16 B operand (lane group q: mins 4q .. 4q+3; groups 2, 3 zero).
-    const uint4 h = cur.h;
-    const float d = f16_ada(h.x & 0xFFFFu), dmin = f16_ada(h.x >> 16);
-    float scl[8], mv[8];
+    // The sub-block scales go into the weight operand: sc_t q (low nibbles)
+    // and (sc_t / 16)(16 q) (high nibbles, which the mask leaves times 16) are
+    // integers up to 945, exact as f16 subnormals times 2^-24, so the column's
+    // eight sub-blocks share one MFMA chain per activation block and d scales
+    // the column once.  The eight mins form an f16 B operand (lane group q:
+    // mins 4q .. 4q+3; groups 2, 3 zero) for the min term.
+    float d[RB], dmin[RB];
+    h8 bw[RB][8];  // [rb][2 gq + nibble]
+    h4 mins[RB];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      uint32_t sc, m;
-      scale_min_k4(h.y, h.z, h.w, t, sc, m);
-      scl[t] = d * (float)sc * ((t & 1) ? 1048576.f : 16777216.f);
-      mv[t] = (float)m;
+    for (int rb = 0; rb < RB; ++rb) {
+      const uint4 h = cur[rb].h;
+      d[rb] = f16_ada(h.x & 0xFFFFu) * 16777216.f;
+      dmin[rb] = f16_ada(h.x >> 16) * (1.f / XSUM_UNIT);
+      float mv[8];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        uint32_t sc0, m0, sc1, m1;
+        scale_min_k4(h.y, h.z, h.w, 2 * gq, sc0, m0);
+        scale_min_k4(h.y, h.z, h.w, 2 * gq + 1, sc1, m1);
+        mv[2 * gq] = (float)m0;
+        mv[2 * gq + 1] = (float)m1;
+        const _Float16 s0 = (_Float16)(float)sc0, s1 = (_Float16)((float)sc1 * 0.0625f);
+        // Codes: bytes 8q .. 8q+7 of the 32-byte group gq, both nibbles.
+        const uint32_t x0 = cur[rb].wc[gq].x, x1 = cur[rb].wc[gq].y, y0 = x0 >> 8, y1 = x1 >> 8;
+        bw[rb][2 * gq] = as_h8(x0 & 0x000F000Fu, y0 & 0x000F000Fu, x1 & 0x000F000Fu, y1 & 0x000F000Fu) * s0;
+        bw[rb][2 * gq + 1] = as_h8(x0 & 0x00F000F0u, y0 & 0x00F000F0u, x1 & 0x00F000F0u, y1 & 0x00F000F0u) * s1;
+      }
+      mins[rb] = as_h4(q == 0 ? pack_h2(mv[0], mv[1]) : q == 1 ? pack_h2(mv[4], mv[5]) : 0u,
+                       q == 0 ? pack_h2(mv[2], mv[3]) : q == 1 ? pack_h2(mv[6], mv[7]) : 0u);
     }
-    const h4 mins = as_h4(q == 0 ? pack_h2(mv[0], mv[1]) : q == 1 ? pack_h2(mv[4], mv[5]) : 0u,
-                          q == 0 ? pack_h2(mv[2], mv[3]) : q == 1 ? pack_h2(mv[6], mv[7]) : 0u);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const _Float16* xr = xb[buf] + (16 * mb + j) * XROW + 8 * q;
       const _Float16* sr = sb[buf] + (16 * mb + j) * SROW + 4 * q;
+      f4 D[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) D[rb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
-        // Codes: bytes 8q .. 8q+7 of the 32-byte group gq, both nibbles.
-        const uint32_t x0 = cur.wc[gq].x, x1 = cur.wc[gq].y, y0 = x0 >> 8, y1 = x1 >> 8;
-        const h8 blo = as_h8(x0 & 0x000F000Fu, y0 & 0x000F000Fu, x1 & 0x000F000Fu, y1 & 0x000F000Fu);
-        const h8 bhi = as_h8(x0 & 0x00F000F0u, y0 & 0x00F000F0u, x1 & 0x00F000F0u, y1 & 0x00F000F0u);
-        f4 D0 = mfma32(lds_h8(xr + 64 * gq), blo, f4{0.f, 0.f, 0.f, 0.f});
-        f4 D1 = mfma32(lds_h8(xr + 64 * gq + 32), bhi, f4{0.f, 0.f, 0.f, 0.f});
-        D0 = mfma32(lds_h8(xr + 256 + 64 * gq), blo, D0);
-        D1 = mfma32(lds_h8(xr + 256 + 64 * gq + 32), bhi, D1);
-        acc[mb] += scl[2 * gq] * D0;
-        acc[mb] += scl[2 * gq + 1] * D1;
+        const h8 a0 = lds_h8(xr + 64 * gq), a1 = lds_h8(xr + 64 * gq + 32);
+        const h8 a2 = lds_h8(xr + 256 + 64 * gq), a3 = lds_h8(xr + 256 + 64 * gq + 32);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          D[rb] = mfma32(a0, bw[rb][2 * gq], D[rb]);
+          D[rb] = mfma32(a1, bw[rb][2 * gq + 1], D[rb]);
+          D[rb] = mfma32(a2, bw[rb][2 * gq], D[rb]);
+          D[rb] = mfma32(a3, bw[rb][2 * gq + 1], D[rb]);
+        }
       }
       // Min terms: acc -= dmin * sum_t m_t * xsum_t.
-      f4 D = mfma16(lds_h4(sr), mins, f4{0.f, 0.f, 0.f, 0.f});
-      D = mfma16(lds_h4(sr + 16), mins, D);
-      acc[mb] -= (dmin * (1.f / XSUM_UNIT)) * D;
+      const h4 s0 = lds_h4(sr), s1 = lds_h4(sr + 16);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        f4 Dm = mfma16(s0, mins[rb], f4{0.f, 0.f, 0.f, 0.f});
+        Dm = mfma16(s1, mins[rb], Dm);
+        acc[rb][mb] += d[rb] * D[rb];
+        acc[rb][mb] -= dmin[rb] * Dm;
+      }
     }
     if (more) {
       xtile_store<MB>(xb[(buf + 1) % NB], sb[(buf + 1) % NB], xv, xsv);
-      cur = nxt;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) cur[rb] = nxt[rb];
     }
     __syncthreads();
   }
-  mm_epilogue<MB>(a, acc);
+  mm_epilogue<MB, RB>(a, acc);
 }
 
 // ---- Q6_K: 16-element sub-blocks, v_mfma_f32_16x16x16f16 ---------------------
@@ -404,9 +446,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       r.wq[ht] = ld4(g + (8 + 2 * hh + t) * 1024 + ro);
     }
   };
-  f4 acc[MB];
+  f4 acc[1][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int mb = 0; mb < MB; ++mb) acc[0][mb] = f4{0.f, 0.f, 0.f, 0.f};
   const int s0 = blockIdx.y * a.spw;
   Q6Regs cur, nxt;
   xu4 xv[XTile<MB>::NX], xsv;
@@ -453,13 +495,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
           // sub-block 8hh + 2k + t: int8 scale byte (2k + t) of the dword pair (sw0, sw1)
           const uint32_t sw = k < 2 ? sw0 : sw1;
           const float sc = (float)(int32_t)__builtin_amdgcn_sbfe(sw, 8 * t + 16 * (k & 1), 8);
-          acc[mb] += (d * sc * 16777216.f) * D[k];
+          acc[0][mb] += (d * sc * 16777216.f) * D[k];
         }
       }
       // Code offset: acc -= 32 d sum_s sc_s xsum_s.
       f4 D = mfma16(lds_h4(sr), scb, f4{0.f, 0.f, 0.f, 0.f});
       D = mfma16(lds_h4(sr + 16), scb, D);
-      acc[mb] -= (32.f * d * (1.f / XSUM_UNIT)) * D;
+      acc[0][mb] -= (32.f * d * (1.f / XSUM_UNIT)) * D;
     }
     if (more) {
       xtile_store<MB>(xb[(buf + 1) % NB], sb[(buf + 1) % NB], xv, xsv);
@@ -482,12 +524,22 @@ static int mm_cus() {
 
 bool mfma_kind(int kind) { return kind == Q4_K || kind == Q6_K; }
 
+// 16-row blocks per wave of the Q4_K kernel: two (a workgroup covers 128
+// rows) for 64 activation rows over at least 128 tiles, so each staged
+// activation tile serves twice the rows (14336x4096, 64 rows: 61 -> 46 us).
+// Smaller products keep one: with half the workgroups they ran slower
+// (4096^2, 64 rows: 22.7 -> 26.9 us; 14336x4096, 32 rows: 31.4 -> 36.2 us).
+static int mm_rb(int kind, int out_dim, int bp) {
+  const int ntiles = (out_dim + 63) / 64;
+  return kind == Q4_K && bp == 64 && ntiles >= 128 && ntiles % 2 == 0 ? 2 : 1;
+}
+
 // Super-block columns per workgroup: the divisor of nsb whose workgroup count
-// (tiles x column groups) is closest to 4 per CU, with at most 256 / Bpad
-// column groups per tile so the final sum keeps every partial in flight.
-static int mm_spw(int in_dim, int out_dim, int bp) {
+// (row groups x column groups) is closest to 4 per CU, with at most 256 / Bpad
+// column groups per row group.
+static int mm_spw(int in_dim, int out_dim, int bp, int rb) {
   static const int cus = mm_cus();
-  const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
+  const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64 / rb;
   const int oks = packed_plan_override_ks();
   if (oks > 0 && nsb % oks == 0 && oks <= 256 / bp) return nsb / oks;
   const double target = 4.0 * cus;
@@ -508,7 +560,9 @@ static int mm_bpad(int batch) { return batch <= 16 ? 16 : batch <= 32 ? 32 : 64;
 
 size_t mfma_workspace_bytes(int in_dim, int out_dim, int batch) {
   const int bp = mm_bpad(batch), nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
-  const int ks = nsb / mm_spw(in_dim, out_dim, bp);
+  // The larger of the two kinds' plans (the buffer serves either).
+  const int ks = std::max(nsb / mm_spw(in_dim, out_dim, bp, mm_rb(Q4_K, out_dim, bp)),
+                          nsb / mm_spw(in_dim, out_dim, bp, 1));
   size_t n = 0;
   n += (size_t)bp * in_dim * 2 * 2;               // xh, xl
   n += (size_t)bp * nsb * 16 * 2 * 2;             // sh, sl
@@ -524,7 +578,8 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
   if (!mfma_kind(kind)) return hipErrorNotSupported;
   if (batch < 1 || batch > 64 || in_dim % 256 || out_dim <= 0) return hipErrorInvalidValue;
   const int bp = mm_bpad(batch), nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
-  const int spw = mm_spw(in_dim, out_dim, bp), ks = nsb / spw;
+  const int rb = mm_rb(kind, out_dim, bp);
+  const int spw = mm_spw(in_dim, out_dim, bp, rb), ks = nsb / spw;
   uint8_t* w = (uint8_t*)work;
   _Float16* xh = (_Float16*)w;
   _Float16* xl = xh + (size_t)bp * in_dim;
@@ -539,19 +594,22 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
   else
     hipLaunchKernelGGL(kq_xsplit<16>, dim3(bp), dim3(1024), 0, s, X, batch, in_dim, xh, xl, sh, sl, inv);
   const MmArgs a{(const uint8_t*)P, nsb, out_dim, batch, spw, xh, xl, sh, sl, inv, Y, part, count, stream_once ? 1 : 0};
-  const dim3 grid(ntiles, ks);
+  const dim3 grid(ntiles / rb, ks);
   // One column per workgroup needs a single activation buffer: half the LDS,
   // so more workgroups are resident at once.
-#define KQ_MM(MB)                                                                                  \
-  if (bp == 16 * MB) {                                                                             \
-    if (spw == 1) {                                                                                \
-      if (kind == Q4_K) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 1>), grid, dim3(256), 0, s, a);     \
-      else hipLaunchKernelGGL((kq_mm_mfma_q6k<MB, 1>), grid, dim3(256), 0, s, a);                  \
-    } else {                                                                                       \
-      if (kind == Q4_K) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 2>), grid, dim3(256), 0, s, a);     \
-      else hipLaunchKernelGGL((kq_mm_mfma_q6k<MB, 2>), grid, dim3(256), 0, s, a);                  \
-    }                                                                                              \
-    return hipGetLastError();                                                                      \
+#define KQ_MM(MB)                                                                                         \
+  if (bp == 16 * MB) {                                                                                    \
+    if (kind == Q4_K && rb == 2) {                                                                        \
+      if (spw == 1) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 1, MB == 1 ? 1 : 2>), grid, dim3(256), 0, s, a); \
+      else hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 2, MB == 1 ? 1 : 2>), grid, dim3(256), 0, s, a);          \
+    } else if (spw == 1) {                                                                                \
+      if (kind == Q4_K) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 1, 1>), grid, dim3(256), 0, s, a);         \
+      else hipLaunchKernelGGL((kq_mm_mfma_q6k<MB, 1>), grid, dim3(256), 0, s, a);                         \
+    } else {                                                                                              \
+      if (kind == Q4_K) hipLaunchKernelGGL((kq_mm_mfma_q4k<MB, 2, 1>), grid, dim3(256), 0, s, a);         \
+      else hipLaunchKernelGGL((kq_mm_mfma_q6k<MB, 2>), grid, dim3(256), 0, s, a);                         \
+    }                                                                                                     \
+    return hipGetLastError();                                                                             \
   }
   KQ_MM(1) KQ_MM(2) KQ_MM(4)
 #undef KQ_MM
