@@ -80,6 +80,18 @@ def load(path=None):
         "aspida_kq_chain_check": (I, [P]),
         "aspida_kq_chain_workgroups": (I, [P]),
         "aspida_kq_chain_destroy": (None, [P]),
+        "aspida_gpu_chain_reset": (None, []),
+        "aspida_gpu_chain_moe": (None, [P, LG, I] * 7 + [P, LG, I, I, I, I]),
+        "aspida_gpu_chain_model": (None, [P, LG, P, LG, P, LG, I, I, I]),
+        "aspida_gpu_chain_ready": (I, []),
+        "aspida_gpu_chain_begin": (None, [P]),
+        "aspida_gpu_chain_end": (None, []),
+        "aspida_gpu_chain_forward": (None, [I, I, P, P]),
+        "aspida_gpu_chain_forward_batch": (None, [I, P, P, P, P]),
+        "aspida_kq_chain_layer": (I, [P, LG, P, LG, P, LG, I]),
+        "aspida_kq_chain_forward_layers": (I, [I, P, I, P]),
+        "aspida_kq_chain_set_graphs": (I, [I]),
+        "aspida_kq_chain_graphs": (I, []),
         "aspida_kq_matmul_workspace": (I, [I, I, I, I, P, P]),
         "aspida_kq_set_packed_plan": (I, [I, I]),
         "aspida_kq_set_mv_engine": (I, [I]),
@@ -166,6 +178,86 @@ class LLMGpu:
         self.lib.aspida_gpu_moe_experts(_p(x), dim, top_k, intermed, n_exp, _p(idx), _p(tw), *args,
                                         _p(sgi), 0 if sgi is None else sgi.size, _p(y))
         return y
+
+
+class ResidentChain:
+    """Python mirror of the Ada chain procedures of LLM_Qwen_GPU
+    (src/llm/llm_qwen_gpu.adb: Chain_Reset, Chain_MoE, Chain_Model,
+    Chain_Ready, Chain_Forward, Chain_Forward_Batch) over the reference's
+    chain ABI, with ``layer`` (aspida_kq_chain_layer) in place of
+    Chain_Dnet / Chain_Fattn.  Weights are copied into HBM at registration,
+    so the arrays may be dropped afterwards.  Matrices are (array, kind)
+    pairs: uint8 GGML bytes, or f32 [out][in] for kind -1.
+    """
+
+    def __init__(self, path=None):
+        self.lib = load(path)
+        self.dim = self.vocab = 0
+
+    def last_error(self):
+        return self.lib.aspida_gpu_last_error()
+
+    def reset(self):
+        self.lib.aspida_gpu_chain_reset()
+        self.dim = self.vocab = 0
+
+    def layer(self, attn_norm, post_norm, mix=None):
+        an = np.ascontiguousarray(attn_norm, np.float32)
+        pn = np.ascontiguousarray(post_norm, np.float32)
+        w, k = (None, 0) if mix is None else mix
+        return self.lib.aspida_kq_chain_layer(_p(an), an.nbytes, _p(pn), pn.nbytes, _p(w),
+                                              0 if w is None else w.nbytes, k)
+
+    def moe(self, router, gate, up, down, shg, shu, shd, n_exp, top_k, intermed, sgi=None):
+        args = []
+        for arr, kind in (router, gate, up, down, shg, shu, shd):
+            args += [_p(arr), arr.nbytes, kind]
+        g = None if sgi is None else np.ascontiguousarray(sgi, np.float32)
+        self.lib.aspida_gpu_chain_moe(*args, _p(g), 0 if g is None else g.nbytes, 0 if g is None else g.size,
+                                      n_exp, top_k, intermed)
+
+    def model(self, embed, fnorm, lm, dim, vocab):
+        e = np.ascontiguousarray(embed, np.float32)
+        f = np.ascontiguousarray(fnorm, np.float32)
+        w, k = lm
+        self.lib.aspida_gpu_chain_model(_p(e), e.nbytes, _p(f), f.nbytes, _p(w), w.nbytes, k, dim, vocab)
+        self.dim, self.vocab = dim, vocab
+
+    def ready(self):
+        return self.lib.aspida_gpu_chain_ready() == 1
+
+    def begin(self):
+        self.lib.aspida_gpu_chain_begin(None)
+
+    def end(self):
+        self.lib.aspida_gpu_chain_end()
+
+    def forward(self, row, pos=0):
+        y = np.empty(self.vocab, np.float32)
+        self.lib.aspida_gpu_chain_forward(int(row), int(pos), None, _p(y))
+        return y
+
+    def forward_batch(self, rows, pos=None):
+        r = np.ascontiguousarray(rows, np.int32)
+        ps = np.zeros(r.size, np.int32) if pos is None else np.ascontiguousarray(pos, np.int32)
+        y = np.empty((r.size, self.vocab), np.float32)
+        self.lib.aspida_gpu_chain_forward_batch(r.size, _p(r), _p(ps), None, _p(y))
+        return y
+
+    def hidden(self, rows, n_layers):
+        """Residual stream [len(rows)][dim] after the first n_layers layers."""
+        r = np.ascontiguousarray(np.atleast_1d(rows), np.int32)
+        h = np.empty((r.size, self.dim), np.float32)
+        rc = self.lib.aspida_kq_chain_forward_layers(r.size, _p(r), n_layers, _p(h))
+        if rc:
+            raise RuntimeError(f"aspida_kq_chain_forward_layers rc={rc}")
+        return h
+
+    def set_graphs(self, on):
+        return self.lib.aspida_kq_chain_set_graphs(1 if on else 0)
+
+    def graphs(self):
+        return self.lib.aspida_kq_chain_graphs()
 
 
 class DeviceOps:

@@ -416,6 +416,12 @@ int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int
 
 }  // namespace
 
+namespace kq {
+// Errors of the resident model chain (kq_model_chain.hip), recorded like this
+// file's own.
+void abi_report(int code, const char* what) { report(code, "%s", what); }
+}  // namespace kq
+
 // =============================================================================
 // Reference ABI
 // =============================================================================

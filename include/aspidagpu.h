@@ -257,6 +257,95 @@ int aspida_kq_chain_check(void *chain);
 int aspida_kq_chain_workgroups(void *chain);
 void aspida_kq_chain_destroy(void *chain);
 
+/* ---- resident model chain (the reference's chain ABI) -----------------------
+ * One decode step of a whole MoE model on device-resident weights: the
+ * embedding row; per layer nx = RMSNorm(H, attn_norm), H += Mix nx, then
+ * nr = RMSNorm(H, post_norm), H += MoE(nr) (LLM_Qwen_Blk.Step,
+ * src/llm/llm_qwen_blk.adb:125-170, with LLM_MoE.Forward's router, top-k and
+ * experts); then logits = LM RMSNorm(H, final_norm) (src/llm/llm_qwen.adb:
+ * 1199-1203).  RMSNorm eps 1e-6.  Weights are given as host pointers and
+ * copied into HBM at registration (quantised matrices repacked, a quantised
+ * router decoded to f32); the chain owns those copies until
+ * aspida_gpu_chain_reset.  The first forward of a lane count runs eagerly;
+ * later ones replay a HIP graph captured after it (ASPIDA_NO_GRAPH in the
+ * environment, or aspida_kq_chain_set_graphs(0), keeps every forward eager).
+ * The reference registers each layer's mixer (attention or delta-net) through
+ * aspida_gpu_chain_fattn / aspida_gpu_chain_dnet, which this library does not
+ * export: a layer and its mixer -- one matvec -- are registered with
+ * aspida_kq_chain_layer instead, so the Ada host's Chain_Available
+ * (src/llm/llm_qwen_gpu.adb:554-560) stays false and it keeps its per-layer
+ * paths.  Errors: registration failures mark the chain not ready
+ * (aspida_gpu_chain_ready() == 0 until a reset); a failed forward fills the
+ * logits with NaN; both set aspida_gpu_last_error. */
+
+/* Drop every registered layer and the model.  Replaces gpu/gpu_matvec.cu:2063-2066. */
+void aspida_gpu_chain_reset(void);
+
+/* Attach the MoE block to the last registered layer (no-op with no layer).
+ * Weight kinds as above (router_k may also be -1: f32 [n_exp][dim]); routed
+ * tensors hold n_exp experts of bytes / n_exp each; sgi is the shared-expert
+ * gate input when sgi_len > 1 (then sgi_len == dim), else the shared expert is
+ * ungated.  n_exp <= 1024, top_k <= 32, intermed % 256 == 0.  Gate, up and
+ * the shared gate/up of one kind and both downs of another run on the grouped
+ * kernels over packed experts, other mixes on the per-projection kernels.
+ * Replaces gpu/gpu_matvec.cu:2143-2199. */
+void aspida_gpu_chain_moe(const void *router_w, long router_b, int router_k,
+                          const void *gate_w, long gate_b, int gate_k,
+                          const void *up_w, long up_b, int up_k,
+                          const void *down_w, long down_b, int down_k,
+                          const void *shg_w, long shg_b, int shg_k,
+                          const void *shu_w, long shu_b, int shu_k,
+                          const void *shd_w, long shd_b, int shd_k,
+                          const float *sgi, long sgi_b, int sgi_len,
+                          int n_exp, int top_k, int intermed);
+
+/* Embedding table (f32 [embed_b / (4 dim)][dim]), final norm (f32 [dim]) and
+ * output head ([vocab][dim] of kind lm_k, -1 = f32).  Replaces
+ * gpu/gpu_matvec.cu:2201-2211. */
+void aspida_gpu_chain_model(const float *embed, long embed_b, const float *fnorm, long fnorm_b,
+                            const void *lm, long lm_b, int lm_k, int dim, int vocab);
+
+/* 1 when a model, at least one layer and no failed registration.  Replaces
+ * gpu/gpu_matvec.cu:2213. */
+int aspida_gpu_chain_ready(void);
+
+/* A generation's start and end: drop the captured graphs.  attn_handles is
+ * unused (the matvec mixers keep no per-generation state).  Replace
+ * gpu/gpu_matvec.cu:2328-2340. */
+void aspida_gpu_chain_begin(const int *attn_handles);
+void aspida_gpu_chain_end(void);
+
+/* logits[vocab] of one token whose embedding row is embed_row; pos and
+ * attn_handles are unused (see aspida_gpu_chain_begin).  Synchronous.
+ * Replaces gpu/gpu_matvec.cu:2356-2400. */
+void aspida_gpu_chain_forward(int embed_row, int pos, const int *attn_handles, float *logits);
+
+/* logits[B][vocab] of B lanes (rows[B]) in one step: the matvecs become
+ * small-batch products and the MoE blocks run the B tokens together (each
+ * expert's weights read once per layer).  1 <= B <= 64 and B * top_k <= 1024;
+ * B < 1 is a no-op as in the reference (which clamped B to its lane limit
+ * instead of failing).  Replaces gpu/gpu_matvec.cu:2783-2961. */
+void aspida_gpu_chain_forward_batch(int B, const int *rows, const int *pos, const int *handles, float *logits);
+
+/* A layer (this library's stand-in for chain_fattn / chain_dnet): attention
+ * and post-attention norms (f32 [dim], an_b = pn_b = 4 dim bytes, dim % 256 ==
+ * 0) and the mixer, a [dim][dim] matrix of kind mix_k (-1 = f32), or none when
+ * mix_w is NULL.  Returns 0 or an error (the chain is then not ready).  No
+ * reference counterpart. */
+int aspida_kq_chain_layer(const float *attn_norm, long an_b, const float *post_norm, long pn_b,
+                          const void *mix_w, long mix_b, int mix_k);
+
+/* The residual stream H[B][dim] after the embedding and the first n_layers
+ * layers (0 <= n_layers <= layer count), run eagerly: the chain's state
+ * step by step.  Returns 0 or an error.  No reference counterpart. */
+int aspida_kq_chain_forward_layers(int B, const int *rows, int n_layers, float *hidden);
+
+/* Graph replay on (1) or off (0) for later forwards; drops captured graphs.
+ * aspida_kq_chain_graphs: graphs currently captured.  No reference
+ * counterpart. */
+int aspida_kq_chain_set_graphs(int on);
+int aspida_kq_chain_graphs(void);
+
 /* ---- GGUF tensor layout (host only) ----------------------------------------
  * A reader of GGUF model files for locating and checking real weights: the
  * header, metadata and tensor descriptors with the reference loader's rules

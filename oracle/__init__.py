@@ -47,6 +47,8 @@ def lib():
         L.kqo_route.restype = None
         L.kqo_moe_experts.argtypes = [P, I, I, I, I, P, P] + [P, I] * 6 + [P, I, P, I]
         L.kqo_moe_forward.argtypes = [P, I, I, I, I, P] + [P, I] * 6 + [P, I, P, P, P, I]
+        L.kqo_rmsnorm.argtypes = [P, P, I, F, P]
+        L.kqo_rmsnorm.restype = None
         _lib = L
     return _lib
 
@@ -205,3 +207,67 @@ def ref_deq_block(kind, blk):
     out = np.empty(256, np.float32)
     L.ref_deq_block(kind, _ptr(blk), _ptr(out))
     return out
+
+
+def rmsnorm(x, w, eps=1e-6):
+    """LLM_RMSNorm.Forward (src/llm/llm_rmsnorm.adb:10-41)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    y = np.empty(x.size, np.float32)
+    lib().kqo_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(y))
+    return y
+
+
+def matvec_any(w, in_dim, out_dim, x):
+    """(array, kind) matrix times x: QMatVec for a quantised kind, the dense
+    ascending-sum matvec for kind -1 (f32 [out][in])."""
+    arr, kind = w
+    if kind == -1:
+        return dense_matvec(np.reshape(arr, (out_dim, in_dim)), x)
+    return qmatvec(kind, arr, in_dim, out_dim, x)
+
+
+def router_f32(router, dim, n_exp):
+    """The f32 [n_exp][dim] router of a MoE block: as given, or decoded from a
+    quantised kind by the Ada decoders (llm_dequant.adb:122-630)."""
+    arr, kind = router
+    if kind == -1:
+        return np.ascontiguousarray(arr, np.float32).reshape(n_exp, dim)
+    return dequant(kind, arr, dim, n_exp)
+
+
+def chain_forward(model, row, n_layers=None, logits=True):
+    """One token through the resident model chain.  Per layer, LLM_Qwen_Blk.Step
+    (src/llm/llm_qwen_blk.adb:125-170): nx = RMSNorm(H, attn_norm), H += Mix nx
+    (the mixer a matvec, the chain's stand-in for attention / delta-net), then
+    nr = RMSNorm(H, post_norm), H += LLM_MoE.Forward(nr) (llm_moe.adb:136-299);
+    at the end logits = LM RMSNorm(H, final_norm) (llm_qwen.adb:1199-1203).
+
+    model: {"embed": f32 [rows][dim], "fnorm": f32 [dim], "lm": (array, kind),
+    "vocab": int, "layers": [{"attn_norm", "post_norm", "mix": (array, kind) or
+    None, "moe": None or {"router": (array, kind), "gate", "up", "down", "shg",
+    "shu", "shd": (array, kind), "sgi": f32 [dim] or None, "n_exp", "top_k",
+    "intermed"}}]}.  Returns (H after n_layers layers, logits or None, the
+    routed experts of each MoE layer as (top_idx, top_w, router logits)).
+    """
+    layers = model["layers"] if n_layers is None else model["layers"][:n_layers]
+    E = np.asarray(model["embed"], np.float32)
+    dim = E.shape[1]
+    H = E[row].copy()
+    routes = []
+    for L in layers:
+        if L.get("mix") is not None:
+            nx = rmsnorm(H, L["attn_norm"])
+            H = (H + matvec_any(L["mix"], dim, dim, nx)).astype(np.float32)
+        M = L.get("moe")
+        if M is not None:
+            nr = rmsnorm(H, L["post_norm"])
+            rw = router_f32(M["router"], dim, M["n_exp"])
+            y, idx, tw = moe_forward(nr, dim, M["intermed"], M["n_exp"], M["top_k"], rw, M["gate"], M["up"],
+                                     M["down"], M["shg"], M["shu"], M["shd"], shared_gate_inp=M.get("sgi"))
+            routes.append((idx, tw, dense_matvec(rw, nr)))
+            H = (H + y).astype(np.float32)
+    out = None
+    if logits:
+        out = matvec_any(model["lm"], dim, model["vocab"], rmsnorm(H, model["fnorm"]))
+    return H, out, routes

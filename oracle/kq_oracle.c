@@ -377,6 +377,20 @@ void kqo_dense_matvec(const float *w, int in_dim, int out_dim, const float *x, f
 
 /* ---- LLM_MoE.Forward (src/llm/llm_moe.adb:111-302) ------------------------ */
 
+/* LLM_RMSNorm.Forward, src/llm/llm_rmsnorm.adb:10-41: Sum_Sq accumulated in
+ * ascending order (a product, then the sum), Rms = Sqrt (Sum_Sq / N + Eps),
+ * y(I) = (x(I) / Rms) * w(I).  The Ada default Eps is 1.0e-6
+ * (llm_rmsnorm.ads:19). */
+void kqo_rmsnorm(const float *x, const float *w, int n, float eps, float *y)
+{
+    float sum_sq = 0.0f;
+    for (int i = 0; i < n; ++i)
+        sum_sq = sum_sq + x[i] * x[i];
+    const float rms = sqrtf(sum_sq / (float)n + eps);
+    for (int i = 0; i < n; ++i)
+        y[i] = (x[i] / rms) * w[i];
+}
+
 static float silu(float v) { return v / (1.0f + expf(-v)); }   /* llm_moe.adb:88 */
 
 /* Steps 2-3 of Forward (llm_moe.adb:153-197), in place on p[n_exp]. */

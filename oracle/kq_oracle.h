@@ -48,6 +48,10 @@ void kqo_dense_matvec(const float *w, int in_dim, int out_dim, const float *x, f
  * for the range [first, last]; returns the number of chunks. */
 int kqo_pool_chunks(int first, int last, int min_grain, int ncpu, int *lo, int *hi);
 
+/* LLM_RMSNorm.Forward: y = (x / sqrt(mean(x^2) + eps)) * w, sum of squares in
+ * ascending order. */
+void kqo_rmsnorm(const float *x, const float *w, int n, float eps, float *y);
+
 /* Router: softmax over logits, greedy top-k (strict >, lowest index wins ties),
  * renormalised weights.  Writes top_idx (0-based) and top_w. */
 void kqo_route(const float *logits, int n_exp, int top_k, int *top_idx, float *top_w);

@@ -187,3 +187,32 @@ def test_matmul_workspace_advisor_shapes(lib):
                                          (aa.Q6_K, 3584, 3584, 65)]:
         alloc, need = _matmul_ws(lib, kind, in_dim, out_dim, batch)
         assert need > 0 and alloc >= need, (kind, in_dim, out_dim, batch, alloc, need)
+
+
+def test_chain_abi_rejects_without_a_model(lib):
+    """The reference chain ABI (aspida_gpu_chain_*) with nothing registered: not ready,
+    a forward reports an error and launches nothing, bad layer arguments are refused
+    before any device work, and reset clears the failure."""
+    lib.aspida_gpu_chain_reset()
+    lib.aspida_gpu_last_error()
+    assert lib.aspida_gpu_chain_ready() == 0
+    y = np.full(4, 7.0, np.float32)
+    lib.aspida_gpu_chain_forward(0, 0, None, y.ctypes.data)
+    assert lib.aspida_gpu_last_error() != 0
+    lib.aspida_gpu_chain_forward_batch(0, None, None, None, y.ctypes.data)      # B < 1: a no-op
+    assert lib.aspida_gpu_last_error() == 0 and np.all(y == 7.0)
+    n = np.ones(300, np.float32)
+    assert lib.aspida_kq_chain_layer(n.ctypes.data, n.nbytes, n.ctypes.data, n.nbytes, None, 0, 0) < 0  # dim % 256
+    m = np.ones(256, np.float32)
+    assert lib.aspida_kq_chain_layer(m.ctypes.data, m.nbytes, n.ctypes.data, n.nbytes, None, 0, 0) < 0  # norms differ
+    assert lib.aspida_kq_chain_layer(m.ctypes.data, m.nbytes, m.ctypes.data, m.nbytes, m.ctypes.data, 0, 9) < 0
+    assert lib.aspida_gpu_last_error() != 0
+    # chain_moe with no layer is a no-op (gpu_matvec.cu:2152), chain_model with a bad kind fails
+    lib.aspida_gpu_chain_reset()
+    lib.aspida_gpu_chain_moe(*([None, 0, 0] * 7), None, 0, 0, 8, 2, 256)
+    assert lib.aspida_gpu_last_error() == 0
+    lib.aspida_gpu_chain_model(m.ctypes.data, m.nbytes, m.ctypes.data, m.nbytes, m.ctypes.data, m.nbytes, 9, 256, 1)
+    assert lib.aspida_gpu_last_error() != 0 and lib.aspida_gpu_chain_ready() == 0
+    lib.aspida_gpu_chain_reset()
+    assert lib.aspida_kq_chain_forward_layers(1, None, 0, None) < 0
+    assert lib.aspida_kq_chain_graphs() == 0

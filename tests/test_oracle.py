@@ -196,3 +196,94 @@ def test_moe_kquant_matches_fp64_recompute():
                            oracle.dequant(gk, shu, dim, inter).astype(np.float64),
                            oracle.dequant(dk, shd, inter, dim).astype(np.float64))
     assert np.max(np.abs(y - want)) <= 1e-4 * np.max(np.abs(want))
+
+
+def test_rmsnorm_closed_forms():
+    """LLM_RMSNorm.Forward (llm_rmsnorm.adb:10-41): for x = c (constant) the
+    output is c / sqrt(c^2 + 1e-6) * w -- at c = 1e-3 the epsilon halves the
+    result, so a dropped or misplaced epsilon fails; for x = a e_j it is
+    a / sqrt(a^2 / n + 1e-6) * w_j, which pins the mean (not the sum)."""
+    gen = np.random.default_rng(5)
+    for n in (256, 2048):
+        w = (1 + 0.5 * gen.standard_normal(n)).astype(np.float32)
+        for c in (3.0, 1e-3, -2.0):
+            y = oracle.rmsnorm(np.full(n, c, np.float32), w)
+            want = c / np.sqrt(np.float64(c) ** 2 + 1e-6) * w.astype(np.float64)
+            assert np.allclose(y, want, rtol=2e-6, atol=0)
+        x = np.zeros(n, np.float32)
+        x[7] = 5.0
+        y = oracle.rmsnorm(x, w)
+        assert y[7] == pytest.approx(5.0 / np.sqrt(25.0 / n + 1e-6) * w[7], rel=2e-6)
+        assert np.count_nonzero(y) == 1
+
+
+def test_rmsnorm_matches_fp64():
+    gen = np.random.default_rng(6)
+    for n in (512, 4096):
+        x = (gen.standard_normal(n) * 3).astype(np.float32)
+        w = gen.standard_normal(n).astype(np.float32)
+        xd = x.astype(np.float64)
+        want = xd / np.sqrt(np.mean(xd * xd) + 1e-6) * w
+        assert np.max(np.abs(oracle.rmsnorm(x, w) - want)) <= 1e-6 * np.max(np.abs(want))
+
+
+def test_chain_forward_matches_fp64_recompute():
+    """oracle.chain_forward against an fp64 recompute of the same model from the
+    oracle's (golden-pinned) dequantized weights: per layer H += Mix norm(H) then
+    H += MoE(norm(H)), then the head on the final norm (llm_qwen_blk.adb:125-170,
+    llm_qwen.adb:1199-1203).  A residual added before its norm, a norm with the
+    other layer weight or a missing residual all fail it."""
+    from aspida_amd import synth
+    gen = synth.rng(21)
+    dim, inter, n_exp, top_k, vocab = 512, 256, 6, 2, 300
+    gk, dk = 0, 1
+
+    def mat(kind, out, inp):
+        return synth.weight_np(kind, out, inp, gen), kind
+    layers = []
+    for li in range(2):
+        layers.append({
+            "attn_norm": (1 + 0.1 * gen.standard_normal(dim)).astype(np.float32),
+            "post_norm": (1 + 0.1 * gen.standard_normal(dim)).astype(np.float32),
+            "mix": mat(gk, dim, dim) if li == 0 else ((gen.standard_normal((dim, dim)) * 0.02).astype(np.float32), -1),
+            "moe": {"router": ((gen.standard_normal((n_exp, dim)) * 0.1).astype(np.float32), -1) if li == 0
+                    else mat(5, n_exp, dim),
+                    "gate": mat(gk, n_exp * inter, dim), "up": mat(gk, n_exp * inter, dim),
+                    "down": mat(dk, n_exp * dim, inter), "shg": mat(gk, inter, dim), "shu": mat(gk, inter, dim),
+                    "shd": mat(dk, dim, inter), "sgi": (gen.standard_normal(dim) * 0.05).astype(np.float32),
+                    "n_exp": n_exp, "top_k": top_k, "intermed": inter}})
+    M = {"embed": gen.standard_normal((4, dim)).astype(np.float32),
+         "fnorm": (1 + 0.1 * gen.standard_normal(dim)).astype(np.float32),
+         "lm": mat(dk, vocab, dim), "vocab": vocab, "layers": layers}
+
+    def deq(w, inp, out):
+        arr, kind = w
+        return (arr.reshape(out, inp) if kind == -1 else oracle.dequant(kind, arr, inp, out)).astype(np.float64)
+
+    def norm(x, w):
+        return x / np.sqrt(np.mean(x * x) + 1e-6) * w.astype(np.float64)
+
+    def ffn(g, u, d, x):
+        a = g @ x
+        return d @ ((a / (1 + np.exp(-a))) * (u @ x))
+    row = 2
+    H = M["embed"][row].astype(np.float64)
+    for L in layers:
+        H = H + deq(L["mix"], dim, dim) @ norm(H, L["attn_norm"])
+        m = L["moe"]
+        nr = norm(H, L["post_norm"])
+        ridx, rw = _route_fp64(deq(m["router"], dim, n_exp) @ nr, top_k)
+        G = deq(m["gate"], dim, n_exp * inter).reshape(n_exp, inter, dim)
+        U = deq(m["up"], dim, n_exp * inter).reshape(n_exp, inter, dim)
+        D = deq(m["down"], inter, n_exp * dim).reshape(n_exp, dim, inter)
+        y = sum(rw[i] * ffn(G[e], U[e], D[e], nr) for i, e in enumerate(ridx))
+        sg = 1 / (1 + np.exp(-(m["sgi"].astype(np.float64) @ nr)))
+        y = y + sg * ffn(deq(m["shg"], dim, inter), deq(m["shu"], dim, inter), deq(m["shd"], inter, dim), nr)
+        H = H + y
+    want = deq(M["lm"], dim, vocab) @ norm(H, M["fnorm"])
+    got_h, got, routes = oracle.chain_forward(M, row)
+    assert len(routes) == 2
+    assert np.max(np.abs(got_h - H)) <= 1e-4 * np.max(np.abs(H))
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want))
+    h1, none, _ = oracle.chain_forward(M, row, n_layers=0, logits=False)
+    assert none is None and np.array_equal(h1, M["embed"][row])
