@@ -934,7 +934,12 @@ static int moe_chunk(int T, int top_k) { return std::min(T, kq::MOE_MAX_JOBS / t
 
 extern "C" long aspida_moe_packed_work_bytes(int T, int dim, int intermed, int top_k) {
   if (T <= 0 || dim <= 0 || intermed <= 0 || top_k <= 0 || top_k > kq::MOE_MAX_TOPK) return -EINVAL;
-  return (long)kq::moe_grouped_work_bytes(moe_chunk(T, top_k), dim, intermed, top_k);
+  size_t n = kq::moe_grouped_work_bytes(moe_chunk(T, top_k), dim, intermed, top_k);
+  // From MOE_PREFILL_MIN_TOKENS tokens the Q4_K / Q6_K experts may take the
+  // prefill products, in launch sequences of up to MOE_PREFILL_MAX_TOKENS.
+  if (T >= kq::MOE_PREFILL_MIN_TOKENS && dim % 256 == 0 && intermed % 256 == 0)
+    n = std::max(n, kq::moe_prefill_work_bytes(std::min(T, kq::MOE_PREFILL_MAX_TOKENS), dim, intermed, top_k));
+  return (long)n;
 }
 
 extern "C" int aspida_moe_pack_experts_dev(int kind, const void* src, long src_stride, int in_dim, int out_dim,
@@ -963,6 +968,9 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
                   kq::moe_grouped_experts_ok(n_exp) &&
                   ((uintptr_t)x & 15) == 0 && ((uintptr_t)work & 255) == 0;
   if (!ok) return -EINVAL;
+  // An error left by earlier work on this thread is reported as such, not as this call's.
+  if (const hipError_t pend = hipGetLastError(); pend != hipSuccess)
+    report((int)pend, "aspida_moe_experts_packed_dev: error pending from earlier work: %s", hipGetErrorString(pend));
   kq::MoeGroupedArgs a{};
   a.gate = (const uint8_t*)gate_p; a.up = (const uint8_t*)up_p; a.down = (const uint8_t*)down_p;
   a.sh_gate = (const uint8_t*)shg_p; a.sh_up = (const uint8_t*)shu_p; a.sh_down = (const uint8_t*)shd_p;
@@ -970,6 +978,21 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
   a.d_stride = kq::packed_bytes(down_kind, intermed, dim);
   a.sgi = shared_gate_inp;
   a.top_k = top_k; a.n_exp = n_exp; a.dim = dim; a.I = intermed;
+  if (kq::moe_prefill_takes(T, gu_kind, down_kind, dim, intermed, top_k, n_exp) && kq::matvec_mfma_takes(gu_kind) &&
+      kq::matvec_mfma_takes(down_kind)) {
+    // Many tokens: the grouped products of kq_moe_prefill.hip, in sequences of
+    // up to MOE_PREFILL_MAX_TOKENS tokens (a last short one included).
+    for (int t0 = 0; t0 < T; t0 += kq::MOE_PREFILL_MAX_TOKENS) {
+      a.T = std::min(kq::MOE_PREFILL_MAX_TOKENS, T - t0);
+      a.x = x + (size_t)t0 * dim;
+      a.idx = top_idx + (size_t)t0 * top_k;
+      a.top_w = top_w + (size_t)t0 * top_k;
+      a.y = y + (size_t)t0 * dim;
+      const int rc = check(kq::launch_moe_prefill(a, work, (hipStream_t)stream), "aspida_moe_experts_packed_dev");
+      if (rc) return rc;
+    }
+    return 0;
+  }
   const int chunk = moe_chunk(T, top_k);
   for (int t0 = 0; t0 < T; t0 += chunk) {
     a.T = std::min(chunk, T - t0);

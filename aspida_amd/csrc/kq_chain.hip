@@ -255,7 +255,8 @@ static int chain_grid() {
     cus = 256;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)kq_chain, 64 * CH_NW, 0) != hipSuccess ||
       per <= 0)
-    per = 1;
+    per = 1;  // fewer workgroups than fit: still all resident
+  (void)hipGetLastError();
   const int G = per * cus / CH_EPOCH_CTRS * CH_EPOCH_CTRS;
   return G > 0 ? G : CH_EPOCH_CTRS;
 }

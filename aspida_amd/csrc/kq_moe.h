@@ -93,6 +93,20 @@ hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kin
 bool moe_mfma_kind(int kind);
 hipError_t launch_moe_grouped_mfma(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
 
+// ---- prefill: many tokens per launch (kq_moe_prefill.hip) ----
+
+// Tokens from which Q4_K gate/up with Q6_K down run the grouped GEMM of
+// kq_moe_prefill.hip, and the most tokens one of its launch sequences takes.
+constexpr int MOE_PREFILL_MIN_TOKENS = 64;
+constexpr int MOE_PREFILL_MAX_TOKENS = 1024;
+bool moe_prefill_takes(int T, int gu_kind, int down_kind, int dim, int I, int top_k, int n_exp);
+// Work bytes of one launch sequence of T <= MOE_PREFILL_MAX_TOKENS tokens
+// (any n_exp up to MOE_MAX_EXP).
+size_t moe_prefill_work_bytes(int T, int dim, int I, int top_k);
+// a: the weights, idx, top_w, x, sgi, y, T, top_k, n_exp, dim, I of
+// MoeGroupedArgs (its work pointers are not used); work 256-byte aligned.
+hipError_t launch_moe_prefill(const MoeGroupedArgs& a, void* work, hipStream_t s);
+
 // Router: logits[t] = router_w[n_exp][dim] . x[t] (f32), stable softmax,
 // greedy top-k (strict >, lowest index wins ties), renormalised weights
 // (llm_moe.adb:136-197).  Writes top_idx/top_w [T][top_k].

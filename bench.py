@@ -17,8 +17,10 @@ captured once in a HIP graph and replayed.
 Printed: one JSON line (metric, value = tokens/s, roofline of the dominant
 kernel measured with HIP events on its stream, cpu_baseline = the C oracle of
 Aspida's CPU QMatVec on the host cores, the per-kind batch-1 matvec table
-at the Llama-3-8B FFN shapes on cold HBM, the small-batch and MoE tables, and
-the same decode stream at Llama-3-70B shape: 80 layers, 44.4 GB per token).
+at the Llama-3-8B FFN shapes on cold HBM, the small-batch and MoE tables, the
+same decode stream at Llama-3-70B shape: 80 layers, 44.4 GB per token, and the
+resident model chain behind the reference chain ABI on a 48-layer
+Qwen3-MoE-shaped model).
 """
 import argparse
 import json
@@ -69,7 +71,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--only", choices=["small", "moe", "kquant", "decode70"],
+    ap.add_argument("--only", choices=["small", "moe", "kquant", "decode70", "chain"],
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
@@ -440,6 +442,68 @@ def moe_table(torch, aa, synth, seed, stream):
     return table
 
 
+def moe_chain_table(aa, synth, seed, tokens=20):
+    """The resident model chain behind the reference's chain ABI
+    (aspida_gpu_chain_moe / _model / _forward / _forward_batch,
+    gpu_matvec.cu:2143-2400, 2783-2961) on a Qwen3-MoE-shaped model: 48 layers,
+    each a Q4_K 2048 x 2048 matvec mixer (the stand-in for attention) and the
+    config-3 MoE block (f32 router [128][2048], 128 experts of Q4_K gate/up
+    [768][2048] and Q6_K down, a gated shared expert, top-8), then the Q6_K
+    output head [151936][2048].  One layer's host weights are registered 48
+    times: every layer gets its own copy in HBM (19 GB).  tok/s is end to end
+    per forward call (row to the device, the graph replay, logits back to the
+    host), at 1 lane and at 8 lanes (8 tokens per call)."""
+    import numpy as np
+    gen = synth.rng(seed + 11)
+    dim, inter, n_exp, top_k, vocab, nlayers, rows = 2048, 768, 128, 8, 151936, 48, 1024
+    ch = aa.ResidentChain()
+    ch.reset()
+    norm = (1.0 + 0.1 * gen.standard_normal(dim)).astype(np.float32)
+    mix = (synth.weight_np(Q4_K, dim, dim, gen), Q4_K)
+    router = ((gen.standard_normal((n_exp, dim)) * 0.02).astype(np.float32), -1)
+    gate = (synth.weight_np(Q4_K, n_exp * inter, dim, gen), Q4_K)
+    up = (synth.weight_np(Q4_K, n_exp * inter, dim, gen), Q4_K)
+    down = (synth.weight_np(Q6_K, n_exp * dim, inter, gen), Q6_K)
+    shg, shu = (synth.weight_np(Q4_K, inter, dim, gen), Q4_K), (synth.weight_np(Q4_K, inter, dim, gen), Q4_K)
+    shd = (synth.weight_np(Q6_K, dim, inter, gen), Q6_K)
+    sgi = (gen.standard_normal(dim) * 0.02).astype(np.float32)
+    for _ in range(nlayers):
+        assert ch.layer(norm, norm, mix) == 0
+        ch.moe(router, gate, up, down, shg, shu, shd, n_exp, top_k, inter, sgi)
+    ch.model(gen.standard_normal((rows, dim)).astype(np.float32), norm, (synth.weight_np(Q6_K, vocab, dim, gen), Q6_K),
+             dim, vocab)
+    assert ch.ready(), f"chain registration failed ({ch.last_error()})"
+    del gate, up, down
+    per_expert = 2 * aa.weight_bytes(Q4_K, dim, inter) + aa.weight_bytes(Q6_K, inter, dim)
+    fixed = aa.weight_bytes(Q4_K, dim, dim) + n_exp * dim * 4     # mixer and router of a layer
+    head = aa.weight_bytes(Q6_K, dim, vocab)
+    out = {}
+    for B in (1, 8):
+        lanes = gen.integers(0, rows, (tokens + 1, B)).astype(np.int32)
+        call = (lambda r: ch.forward(int(r[0]))) if B == 1 else (lambda r: ch.forward_batch(r))
+        y = call(lanes[0])                                        # eager run, then the graph capture
+        assert np.all(np.isfinite(y)) and ch.graphs() >= 1
+        t0 = time.perf_counter()
+        for r in lanes[1:]:
+            call(r)
+        t = (time.perf_counter() - t0) / tokens
+        assert ch.last_error() == 0
+        # Weight bytes per call: the experts the lanes' tokens touch are counted as
+        # distinct per layer when B = 1 (top-8 + shared); for B lanes as the expected
+        # number of distinct experts among B * 8 uniform picks (an estimate).
+        distinct = top_k if B == 1 else n_exp * (1 - (1 - top_k / n_exp) ** B)
+        nbytes = nlayers * (fixed + (distinct + 1) * per_expert) + head
+        out[f"B={B}"] = {"tok_s": round(B / t, 1), "ms_per_call": round(t * 1e3, 3),
+                         "weight_bytes_per_call": int(nbytes),
+                         "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3)}
+        print(f"# MoE chain B={B}: {B / t:.1f} tok/s, {t * 1e3:.3f} ms per call", file=sys.stderr, flush=True)
+    ch.reset()
+    out["model"] = {"layers": nlayers, "dim": dim, "experts": n_exp, "expert_ffn": inter, "top_k": top_k,
+                    "shared_expert": True, "mixer": "Q4_K 2048x2048 matvec (stand-in for attention)",
+                    "vocab": vocab, "head": "Q6_K", "tokens": tokens, "graph_replay": True}
+    return out
+
+
 def abi_path(aa, synth, seed, tokens=4):
     """The drop-in ABI as the reference's callers use it (LLM_GPU over
     aspida_gpu_matvec, gpu_matvec.cu:508-529): host x in, host y out, so each
@@ -665,6 +729,9 @@ def main():
     if args.only:
         if args.copy_probe_mib:
             copy_probe(torch, args.copy_probe_mib)
+        if args.only == "chain":
+            print(json.dumps({"moe_chain": moe_chain_table(aa, synth, args.seed)}), flush=True)
+            return
         fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
         return
@@ -710,6 +777,7 @@ def main():
                                               args.warmup)
 
     abi = None if args.no_table else abi_path(aa, synth, args.seed)
+    mchain = None if args.no_table else moe_chain_table(aa, synth, args.seed)
 
     cpu = None
     if not args.no_cpu:
@@ -750,6 +818,7 @@ def main():
         "kquant_matvec": table,
         "small_batch": small,
         "moe_layer": moe,
+        "moe_chain": mchain,
         "decode_70b": big,
     }
     assert dec_bytes_ok(MODEL_8B), "weight stream size drifted from the Llama-3-8B Q4_K_M layout"
