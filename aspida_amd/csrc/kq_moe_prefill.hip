@@ -261,6 +261,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   }
 }
 
+// Down for intermediate sizes of at most PF_DN_COLS super-block columns: the
+// group's activations for every column are staged in LDS once per pass of
+// 16 MB jobs, then the workgroup walks PF_DN_TILES 64-row tiles of dim
+// against them -- the next tile's weights in flight while the current one is
+// multiplied, and no barrier between tiles.
+constexpr int PF_DN_COLS = 3;
+constexpr int PF_DN_TILES = 8;
+
+template <int MB, int BPG>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void moe_pf_down_wide(PfArgs a) {
+  constexpr int GB = 64 * 210, BP = 16 * MB, NC = PF_DN_COLS;
+  __shared__ __attribute__((aligned(16))) _Float16 xb[NC][BP * XROW];
+  __shared__ __attribute__((aligned(16))) _Float16 sb[NC][BP * SROW];
+  __shared__ int jb[BPG], rows[BPG];
+  const int tiles = a.dim / 64, blocks = (tiles + PF_DN_TILES - 1) / PF_DN_TILES, nsb = a.I / 256;
+  const int c = blockIdx.x / blocks, tb = blockIdx.x % blocks;
+  int4 G;
+  if (!pf_group<BPG>(a, c, false, jb, rows, G)) return;
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e = G.x, row = 16 * w + j;
+  const uint8_t* Wd = e == a.n_exp ? a.sh_down : a.down + (size_t)e * a.d_stride;
+  const int t0 = tb * PF_DN_TILES, t1 = std::min(tiles, t0 + PF_DN_TILES);
+  auto load_tile = [&](int tile, Q6Regs (&r)[NC]) {
+#pragma unroll
+    for (int s = 0; s < NC; ++s)
+      if (s < nsb) q6k_load(Wd + ((size_t)tile * nsb + s) * GB, row, q, r[s]);
+  };
+  for (int base = 0; base < G.z; base += BP) {
+    Q6Regs cur[NC], nxt[NC];
+    load_tile(t0, cur);
+    {
+      xu4 xv[XTile<MB>::NX], xsv;
+#pragma unroll
+      for (int s = 0; s < NC; ++s)
+        if (s < nsb) {
+          pf_xload<MB>(a.hh, a.hl, a.hsh, a.hsl, nsb, rows + base, s, xv, xsv);
+          xtile_store<MB>(xb[s], sb[s], xv, xsv);
+        }
+    }
+    __syncthreads();
+    for (int tile = t0; tile < t1; ++tile) {
+      if (tile + 1 < t1) load_tile(tile + 1, nxt);
+      f4 acc[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NC; ++s)
+        if (s < nsb) q6k_column<MB>(cur[s], xb[s], sb[s], j, q, acc);
+      const int orow = 64 * tile + row;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int b = base + 16 * mb + 4 * q + r, job = b < BPG ? jb[b] : -1;
+          if (job >= 0) a.yk[(size_t)job * a.dim + orow] = acc[mb][r] * a.hinv[job];
+        }
+      if (tile + 1 < t1)
+#pragma unroll
+        for (int s = 0; s < NC; ++s) cur[s] = nxt[s];
+    }
+    __syncthreads();  // the next pass overwrites the staged activations
+  }
+}
+
 // y[t][row] = sum_k top_w[t][k] yk[t slots + k][row] (ascending k) +
 // g_t yk[t slots + top_k][row], g_t = sigmoid(sgi . x_t) or 1 without sgi
 // (llm_moe.adb:270-299).  Workgroup (i, t): rows 256 i .. 256 i + 255 of
@@ -385,6 +450,8 @@ hipError_t launch_moe_prefill(const MoeGroupedArgs& g, void* work, hipStream_t s
     default: hipLaunchKernelGGL(moe_pf_plan<64>, dim3(1), dim3(1024), 0, s, a); break;
   }
   const dim3 gu((unsigned)(groups * (a.I / 64))), dn((unsigned)(groups * (a.dim / 64)));
+  const bool wide = a.I / 256 <= PF_DN_COLS;
+  const dim3 dnw((unsigned)(groups * ((a.dim / 64 + PF_DN_TILES - 1) / PF_DN_TILES)));
   switch (mb) {
     case 1: hipLaunchKernelGGL(moe_pf_gate_up<1>, gu, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL(moe_pf_gate_up<2>, gu, dim3(256), 0, s, a); break;
@@ -392,10 +459,18 @@ hipError_t launch_moe_prefill(const MoeGroupedArgs& g, void* work, hipStream_t s
   }
   e = launch_xsplit(16, a.h, J, J, a.I, a.hh, a.hl, a.hsh, a.hsl, a.hinv, s);
   if (e != hipSuccess) return e;
-  switch (mb) {
-    case 1: hipLaunchKernelGGL((moe_pf_down<1, 16>), dn, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((moe_pf_down<2, 32>), dn, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((moe_pf_down<2, 64>), dn, dim3(256), 0, s, a); break;
+  if (wide) {
+    switch (mb) {
+      case 1: hipLaunchKernelGGL((moe_pf_down_wide<1, 16>), dnw, dim3(256), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((moe_pf_down_wide<2, 32>), dnw, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL((moe_pf_down_wide<2, 64>), dnw, dim3(256), 0, s, a); break;
+    }
+  } else {
+    switch (mb) {
+      case 1: hipLaunchKernelGGL((moe_pf_down<1, 16>), dn, dim3(256), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((moe_pf_down<2, 32>), dn, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL((moe_pf_down<2, 64>), dn, dim3(256), 0, s, a); break;
+    }
   }
   hipLaunchKernelGGL(moe_pf_combine, dim3((a.dim + 255) / 256, a.T), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -112,12 +112,12 @@ def test_grouped_moe_rejects_bad_arguments(lib):
     sched = ((1024 + 2 + 9) * 4 + 255) // 256 * 256
     table = (1 + (9 + 1) // 2 + 8 + 1) * 16
     assert lib.aspida_moe_packed_work_bytes(1, 2048, 768, 8) == 4 * 9 * (768 + 2048) + 256 + 128 * 256 + sched + table
-    # From 64 tokens the Q4_K / Q6_K experts may take the prefill products, in sequences of at
+    # From 96 tokens the Q4_K / Q6_K experts may take the prefill products, in sequences of at
     # most 1024 tokens: the size grows with T up to 1024 tokens and no further
-    ws = [lib.aspida_moe_packed_work_bytes(T, 2048, 768, 8) for T in (32, 64, 512, 1024, 1025, 5000)]
+    ws = [lib.aspida_moe_packed_work_bytes(T, 2048, 768, 8) for T in (32, 96, 512, 1024, 1025, 5000)]
     assert ws[0] < ws[1] < ws[2] < ws[3] == ws[4] == ws[5]
-    # below 64 tokens, T * top_k above the per-launch job bound: sized for one chunk of 128 jobs' tokens
-    assert lib.aspida_moe_packed_work_bytes(63, 512, 256, 32) == lib.aspida_moe_packed_work_bytes(32, 512, 256, 32)
+    # below 96 tokens, T * top_k above the per-launch job bound: sized for one chunk of 1024 jobs' tokens
+    assert lib.aspida_moe_packed_work_bytes(95, 512, 256, 32) == lib.aspida_moe_packed_work_bytes(32, 512, 256, 32)
     one = 256
     args = dict(x=one, T=1, dim=2048, top_k=8, intermed=768, n_exp=128, idx=one, tw=one, g=one, u=one, gk=0, d=one,
                 dk=1, sg=one, su=one, sd=one, sgi=None, work=one, y=one)

@@ -262,8 +262,8 @@ PACKED_CASES = [
     (1792, 1792, 5, 2, aa.Q2_K, aa.Q8_0, False, 9),     # 7 columns: 1 wave x 7
     (256, 256, 3, 2, aa.Q6_K, aa.Q4_K, True, 130),      # one column; 87 jobs per expert
     (512, 768, 8, 4, aa.Q8_0, aa.Q5_K, True, 300),      # T * top_k > 1024: two launches
-    # Q4_K / Q6_K from 64 tokens: the grouped prefill products (kq_moe_prefill.hip)
-    (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 64),    # 16-job groups
+    # Q4_K / Q6_K from 96 tokens: the grouped prefill products (kq_moe_prefill.hip)
+    (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 96),    # 16-job groups
     (1024, 512, 16, 2, aa.Q4_K, aa.Q6_K, True, 150),    # 16-job groups, ~19 jobs per expert
     (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 700),   # 64-job groups
     (512, 256, 8, 4, aa.Q4_K, aa.Q6_K, False, 1100),    # two sequences: 1024 tokens, then 76 (32-job groups)
@@ -351,10 +351,10 @@ def test_moe_experts_packed_repeated_expert():
 
 
 def test_moe_prefill_repeated_and_invalid_experts():
-    """The prefill products (T >= 64): a token that lists one expert twice gets
+    """The prefill products (T >= 96): a token that lists one expert twice gets
     both contributions, and a token with an expert id outside [0, n_exp)
     keeps its y unwritten while every other token is still right."""
-    dim, inter, n_exp, top_k, T = 512, 256, 4, 3, 80
+    dim, inter, n_exp, top_k, T = 512, 256, 4, 3, 100
     dev = aa.DeviceOps()
     gen = synth.rng(1888)
     L = _layer(gen, dim, inter, n_exp)
@@ -367,7 +367,7 @@ def test_moe_prefill_repeated_and_invalid_experts():
     idx[17] = [1, n_exp + 3, 0]
     y, _ = _run_packed(dev, L, dim, inter, n_exp, top_k, aa.Q4_K, aa.Q6_K, True, X, idx, tw)
     assert np.all(np.isnan(y[17])), "a token with an invalid expert was written"
-    for t in (0, 5, 16, 18, 79):
+    for t in (0, 5, 16, 18, 99):
         want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, idx[t], tw[t], L["gate"], L["up"], L["down"],
                                   L["shg"], L["shu"], L["shd"], shared_gate_inp=L["sgi"], nthreads=ncpu())
         _assert_moe(y[t], want, f"token {t}")
