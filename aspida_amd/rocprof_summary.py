@@ -35,8 +35,9 @@ import statistics
 
 
 def short_name(name):
-    """'void kq::kq_mv_packed<0, 16>(unsigned char const*, ...)' -> 'kq_mv_packed<0, 16>'."""
-    head = name.split("(")[0]
+    """'void kq::kq_mv_packed<0, 16>(unsigned char const*, ...)' -> 'kq_mv_packed<0, 16>'
+    ('(anonymous namespace)::' scopes dropped first)."""
+    head = name.replace("(anonymous namespace)::", "").split("(")[0]
     head = re.sub(r"^void\s+", "", head)
     return head.split("::")[-1] if "::" in head else head
 

@@ -60,6 +60,8 @@ def layer_plan(m=MODEL_8B):
 
 # Launches of one layer: q|k and v share their input and run as one launch.
 LAYER_LAUNCHES = [("qk", "v"), ("o",), ("gate_up",), ("down",)]
+# Token counts of the MoE prefill rows (the grouped-GEMM path from 96 tokens).
+PREFILL_TOKENS = (128, 256, 512, 1024)
 
 
 def parse():
@@ -71,7 +73,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--only", choices=["small", "moe", "kquant", "decode70", "chain"],
+    ap.add_argument("--only", choices=["small", "moe", "kquant", "decode70", "chain", "prefill"],
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
@@ -362,14 +364,16 @@ def small_batch_kernel(aa, kind, inp, out, B):
     return "kq_mm_mfma"
 
 
-def moe_table(torch, aa, synth, seed, stream):
+def moe_table(torch, aa, synth, seed, stream, tokens=(1, 8, 32), tag="MoE"):
     """Qwen3-MoE-style expert FFN: router f32 [128][2048],
     128 experts of gate/up Q4_K [768][2048] and down Q6_K [2048][768] plus one
     shared expert with a sigmoid gate, top-8, for T = 1, 8 and 32 tokens; the
     device path (router + grouped experts over packed expert tensors),
     rotating over three layers' weights (1.2 GB) so each layer reads cold HBM.
     GB/s counts the weights of the E_T distinct routed experts the router
-    picked, the shared expert, the router and the activations."""
+    picked, the shared expert, the router and the activations; TFLOP/s counts
+    2 T (top_k + 1) 3 dim I, the experts' multiply-adds (the prefill rows,
+    `tokens` = 128 .. 1024, are compute-bound)."""
     dev = aa.DeviceOps()
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 3)
@@ -396,7 +400,7 @@ def moe_table(torch, aa, synth, seed, stream):
     ds = aa.weight_bytes(aa.Q6_K, inter, dim)
     per_expert = 2 * gs + ds
     table = {}
-    for T in (1, 8, 32):
+    for T in tokens:
         X = torch.randn(T, dim, generator=g, **f)
         bufs = [{"logits": torch.empty(T, n_exp, **f), "idx": torch.empty(T, top_k, device="cuda", dtype=torch.int32),
                  "tw": torch.empty(T, top_k, **f),
@@ -432,10 +436,12 @@ def moe_table(torch, aa, synth, seed, stream):
         t = e0.elapsed_time(e1) * 1e-3 / (reps * nlayers)
         distinct = sum(len(set(B["idx"].cpu().numpy().ravel().tolist())) for B in bufs) / nlayers
         nbytes = (distinct + 1) * per_expert + n_exp * dim * 4 + 4 * T * (2 * dim)
+        flops = 2.0 * T * (top_k + 1) * 3 * dim * inter
         table[f"T={T}"] = {"us": round(t * 1e6, 2), "distinct_experts": round(distinct, 1),
-                           "GBps": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3)}
-        print(f"# MoE T={T}: {t * 1e6:.2f} us, E_T={distinct:.1f}, {nbytes / t / 1e9:.0f} GB/s",
-              file=sys.stderr, flush=True)
+                           "GBps": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3),
+                           "tok_s": round(T / t, 1), "TFLOPs": round(flops / t / 1e12, 2)}
+        print(f"# {tag} T={T}: {t * 1e6:.2f} us, E_T={distinct:.1f}, {nbytes / t / 1e9:.0f} GB/s, "
+              f"{flops / t / 1e12:.1f} TFLOP/s", file=sys.stderr, flush=True)
         del graph, bufs
     del layers
     torch.cuda.empty_cache()
@@ -732,6 +738,10 @@ def main():
         if args.only == "chain":
             print(json.dumps({"moe_chain": moe_chain_table(aa, synth, args.seed)}), flush=True)
             return
+        if args.only == "prefill":
+            print(json.dumps({"moe_prefill": moe_table(torch, aa, synth, args.seed, stream, PREFILL_TOKENS,
+                                                        "MoE prefill")}), flush=True)
+            return
         fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
         return
@@ -771,6 +781,7 @@ def main():
     table = None if args.no_table else kquant_table(torch, aa, synth, args.seed, stream)
     small = None if args.no_table else small_batch_table(torch, aa, synth, args.seed, stream)
     moe = None if args.no_table else moe_table(torch, aa, synth, args.seed, stream)
+    prefill = None if args.no_table else moe_table(torch, aa, synth, args.seed, stream, PREFILL_TOKENS, "MoE prefill")
     del dec
     torch.cuda.empty_cache()
     big = None if args.no_70b else decode_70b(torch, aa, synth, args.seed, stream, args.mv_engine, args.steps,
@@ -818,6 +829,7 @@ def main():
         "kquant_matvec": table,
         "small_batch": small,
         "moe_layer": moe,
+        "moe_prefill": prefill,
         "moe_chain": mchain,
         "decode_70b": big,
     }
