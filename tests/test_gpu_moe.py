@@ -161,12 +161,14 @@ def test_moe_shared_gate_input_read_per_call(kinds):
     _free(gpu, L)
 
 
-@pytest.mark.parametrize("T", [1, 8, 32])
-def test_router_selection_matches_oracle(T):
+@pytest.mark.parametrize("T,n_exp,dim", [(1, 128, 2048), (8, 128, 2048), (32, 128, 2048), (203, 128, 2048),
+                                         (400, 128, 2048), (522, 300, 1536),  # token-group router from 384 tokens
+                                         (390, 64, 4096)])                    # dim above its limit: expert split
+def test_router_selection_matches_oracle(T, n_exp, dim):
     torch = torch_cuda()
     dev = aa.DeviceOps()
     gen = synth.rng(900 + T)
-    n_exp, dim, top_k = 128, 2048, 8
+    top_k = 8
     W = (gen.standard_normal((n_exp, dim)) * 0.02).astype(np.float32)
     X = synth.activations_np(T * dim, gen).reshape(T, dim)
     dW, dX = to_dev(W), to_dev(X)
