@@ -12,10 +12,12 @@
 //   moe_pf_gate_up  per (group, 64-row tile): gate and up rows of the group's
 //                   expert against the group's activation rows, gathered by
 //                   token; h[job][row] = silu(gate) * up
+//   moe_pf_gates    the tokens' shared-expert gates g_t, one wave per token
 //   kq_xsplit<16>   h as f16 hi / lo images, one row per job
 //   moe_pf_down     per (group, 64-row tile of dim): yk[job][row] = down . h[job]
 //   moe_pf_combine  y[t] = sum_k top_w[t][k] yk[t, k] (ascending k) +
 //                   g_t yk[t, shared], g_t = sigmoid(shared_gate_inp . x_t)
+//                   (1 without shared_gate_inp)
 //
 // Each product tile reads its 64 weight rows once for up to BP = 64 jobs, so
 // the weights of an expert are read once per BP of its jobs rather than once
@@ -45,6 +47,7 @@ struct PfArgs {
   // work
   _Float16 *xh, *xl, *xsh, *xsl;
   float* xinv;
+  float* gsh;   // [T] shared-expert gates
   float* h;
   _Float16 *hh, *hl, *hsh, *hsl;
   float* hinv;
@@ -144,6 +147,30 @@ __device__ __forceinline__ bool pf_group(const PfArgs& a, int c, bool by_token, 
   }
   __syncthreads();
   return true;
+}
+
+// The shared-expert gates g_t = sigmoid(sgi . x_t), or 1 without sgi
+// (llm_moe.adb:285-293), one wave per token.  A launch of its own: inside the
+// gate/up kernel its registers cost the 32-job variant its second wave per
+// SIMD (T = 512: 470 -> 541 us per layer).
+__global__ __launch_bounds__(256) void moe_pf_gates(PfArgs a) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int t = blockIdx.x * 4 + w; t < a.T; t += gridDim.x * 4) {
+    float s = 0.f;
+    if (a.sgi) {
+      const float4* g4 = reinterpret_cast<const float4*>(a.sgi);
+      const float4* x4 = reinterpret_cast<const float4*>(a.x + (size_t)t * a.dim);
+      for (int i = lane; i < a.dim / 4; i += 64) {
+        const float4 gv = g4[i], xv = x4[i];
+        s = __builtin_fmaf(gv.x, xv.x, s);
+        s = __builtin_fmaf(gv.y, xv.y, s);
+        s = __builtin_fmaf(gv.z, xv.z, s);
+        s = __builtin_fmaf(gv.w, xv.w, s);
+      }
+      s = wave_total(s);
+    }
+    if (lane == 0) a.gsh[t] = a.sgi ? 1.0f / (1.0f + expf(-s)) : 1.0f;
+  }
 }
 
 // Gate and up of one (group, 64-row tile): wave w takes rows 16 w .. 16 w + 15
@@ -327,30 +354,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 }
 
 // y[t][row] = sum_k top_w[t][k] yk[t slots + k][row] (ascending k) +
-// g_t yk[t slots + top_k][row], g_t = sigmoid(sgi . x_t) or 1 without sgi
-// (llm_moe.adb:270-299).  Workgroup (i, t): rows 256 i .. 256 i + 255 of
-// token t; each workgroup forms g_t itself (a dim-long dot).  A token with a
-// routed expert outside [0, n_exp) keeps its y unwritten.
+// g_t yk[t slots + top_k][row] (llm_moe.adb:270-299), g_t from
+// moe_pf_gates.  Workgroup (i, t): rows 256 i .. 256 i + 255 of token t.  A token
+// with a routed expert outside [0, n_exp) keeps its y unwritten.
 __global__ __launch_bounds__(256) void moe_pf_combine(PfArgs a) {
-  __shared__ float part[4];
   const int t = blockIdx.y, row = blockIdx.x * 256 + threadIdx.x, slots = a.top_k + 1;
   bool ok = true;
   for (int k = 0; k < a.top_k; ++k) {
     const int e = a.idx[(size_t)t * a.top_k + k];
     ok = ok && e >= 0 && e < a.n_exp;
   }
-  if (!ok) return;
-  float gs = 1.f;
-  if (a.sgi) {
-    const float* xt = a.x + (size_t)t * a.dim;
-    float s = 0.f;
-    for (int i = threadIdx.x; i < a.dim; i += 256) s = __builtin_fmaf(a.sgi[i], xt[i], s);
-    s = wave_total(s);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
-    __syncthreads();
-    gs = 1.0f / (1.0f + expf(-(((part[0] + part[1]) + part[2]) + part[3])));
-  }
-  if (row >= a.dim) return;
+  if (!ok || row >= a.dim) return;
+  const float gs = a.gsh[t];
   const float* yt = a.yk + (size_t)t * slots * a.dim + row;
   float acc = 0.f;
   for (int k0 = 0; k0 < a.top_k; k0 += 8) {
@@ -385,6 +400,7 @@ size_t moe_prefill_work_bytes(int T, int dim, int I, int top_k) {
   n += 2 * pf_round((size_t)T * dim * 2);       // xh, xl
   n += 2 * pf_round((size_t)T * nd * 16 * 2);   // xsh, xsl
   n += pf_round((size_t)T * 4);                 // xinv
+  n += pf_round((size_t)T * 4);                 // gsh
   n += pf_round(J * I * 4);                     // h
   n += 2 * pf_round(J * I * 2);                 // hh, hl
   n += 2 * pf_round(J * ni * 16 * 2);           // hsh, hsl
@@ -408,6 +424,7 @@ static void pf_bind(PfArgs& a, void* work) {
   a.xsh = (_Float16*)take((size_t)a.T * nd * 16 * 2);
   a.xsl = (_Float16*)take((size_t)a.T * nd * 16 * 2);
   a.xinv = (float*)take((size_t)a.T * 4);
+  a.gsh = (float*)take((size_t)a.T * 4);
   a.h = (float*)take(J * a.I * 4);
   a.hh = (_Float16*)take(J * a.I * 2);
   a.hl = (_Float16*)take(J * a.I * 2);
@@ -472,6 +489,7 @@ hipError_t launch_moe_prefill(const MoeGroupedArgs& g, void* work, hipStream_t s
       default: hipLaunchKernelGGL((moe_pf_down<2, 64>), dn, dim3(256), 0, s, a); break;
     }
   }
+  hipLaunchKernelGGL(moe_pf_gates, dim3((a.T + 3) / 4), dim3(256), 0, s, a);
   hipLaunchKernelGGL(moe_pf_combine, dim3((a.dim + 255) / 256, a.T), dim3(256), 0, s, a);
   return hipGetLastError();
 }
