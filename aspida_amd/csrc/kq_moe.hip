@@ -268,11 +268,139 @@ __device__ __forceinline__ void route_select(const float* lg, int n_exp, int top
   }
 }
 
+// The same selection by the four waves of the last workgroup, for
+// n_exp <= 64 PER <= 256: the greedy rounds above are a chain of dependent
+// cross-lane steps (8 rounds took 3 us on MI355X), while this is a rank count
+// whose steps are independent.  The nt <= 4 tokens of the workgroup share its
+// waves: G = 4, 2 or 1 waves per token.  Every wave computes its token's
+// probabilities exactly as route_select does (same loads, max, exp, sum and
+// division), so they are bit-identical.  Expert e gets the key
+// (bits(p_e) << 32) | ~e: the probabilities are >= 0, so comparing keys as
+// unsigned integers orders by p and puts the lower index first among equal
+// p -- the CPU's strict > rule -- and rank(e) = #{j : key_j > key_e} is the
+// round in which the greedy loop picks e.  The G waves of a token count over
+// 1 / G of the experts each; the experts of rank < top_k are the selection,
+// renormalised in ascending rank as route_select does.  A token with a NaN
+// probability takes route_select (its rule for NaN is not a rank).  All 256
+// threads call this; the logits are another workgroup's output (device-scope
+// loads).
+constexpr int ROUTE_RANK_MAX = 256;
+struct RouteLds {
+  unsigned long long key[ROUTE_TT][ROUTE_RANK_MAX];
+  unsigned short part[4][ROUTE_RANK_MAX];
+  float selp[ROUTE_TT][64];
+  int seli[ROUTE_TT][64];
+  int has_nan[ROUTE_TT];
+};
+
+template <int PER, int G>
+__device__ __forceinline__ void route_select_wg(RouteLds& L, const float* logits, int n_exp, int top_k, int t0,
+                                                int nt, int* __restrict__ top_idx, float* __restrict__ top_w) {
+  constexpr int NE = 64 * PER;
+  static_assert(NE <= ROUTE_RANK_MAX, "rank selection up to 256 experts");
+  auto& key = L.key;
+  auto& part = L.part;
+  auto& selp = L.selp;
+  auto& seli = L.seli;
+  auto& has_nan = L.has_nan;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tt = w / G, sw = w % G;
+  const bool active = tt < nt;
+  const float* lg = logits + (size_t)(t0 + (active ? tt : 0)) * n_exp;
+  float p[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = __hip_atomic_load(lg + (e < n_exp ? e : n_exp - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (lane + 64 * i >= n_exp) p[i] = -INFINITY;
+    m = fmaxf(m, p[i]);
+  }
+  m = wave_max(m);
+  float part_sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    p[i] = lane + 64 * i < n_exp ? expf(p[i] - m) : 0.f;
+    part_sum += p[i];
+  }
+  const float sum = wave_total(part_sum);
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = p[i] / sum;
+    nan = nan || (e < n_exp && __builtin_isnan(p[i]));
+    if (active && sw == 0) key[tt][e] = e < n_exp ? ((unsigned long long)__float_as_uint(p[i]) << 32) | (unsigned)~e : 0ull;
+  }
+  if (threadIdx.x < ROUTE_TT) has_nan[threadIdx.x] = 0;
+  __syncthreads();
+  if (active && sw == 0 && nan) has_nan[tt] = 1;
+  __syncthreads();
+  const bool rank = active && !has_nan[tt];
+  // Wave (tt, sw) counts the keys j in [q sw, q sw + q) above each of its
+  // lane's keys.
+  if (rank) {
+    constexpr int Q = NE / G;  // keys per wave: a compile-time count, so the LDS reads are issued ahead
+    unsigned cnt[PER];
+    unsigned long long mine[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      cnt[i] = 0;
+      mine[i] = key[tt][lane + 64 * i];
+    }
+    const unsigned long long* kq = &key[tt][Q * sw];
+#pragma unroll 16
+    for (int j = 0; j < Q; ++j) {
+      const unsigned long long kj = kq[j];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) cnt[i] += kj > mine[i] ? 1u : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) part[w][lane + 64 * i] = (unsigned short)cnt[i];
+  }
+  __syncthreads();
+  if (rank && sw == 0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = lane + 64 * i;
+      int r = 0;
+      for (int g = 0; g < G; ++g) r += part[w + g][e];
+      if (e < n_exp && r < top_k) {
+        selp[tt][r] = p[i];
+        seli[tt][r] = e;
+      }
+    }
+  }
+  __syncthreads();
+  if (!active || sw != 0) return;
+  int* idx = top_idx + (size_t)(t0 + tt) * top_k;
+  float* tw = top_w + (size_t)(t0 + tt) * top_k;
+  if (!rank) {
+    route_select<PER>(lg, n_exp, top_k, lane, idx, tw);
+    return;
+  }
+  // Renormalise by the sum of the selected probabilities, in ascending k
+  // (lane k holds the k-th; top_k <= 64).
+  const float pk = lane < top_k ? selp[tt][lane] : 0.f;
+  const int ik = lane < top_k ? seli[tt][lane] : 0;
+  float swt = 0.f;
+  for (int k = 0; k < top_k; ++k) swt = swt + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), k));
+  if (lane < top_k) {
+    idx[lane] = ik;
+    tw[lane] = pk / swt;
+  }
+}
+
 __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, int n_exp, int dim, int T,
                                                  const float* __restrict__ x, int top_k, float* __restrict__ logits,
                                                  int* __restrict__ top_idx, float* __restrict__ top_w,
                                                  unsigned* __restrict__ count) {
   __shared__ int last;
+  __shared__ RouteLds sel;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int e = blockIdx.x * 4 + w;
@@ -328,7 +456,21 @@ __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, in
     last = l;
   }
   __syncthreads();
-  if (!last || w >= nt) return;
+  if (!last) return;
+  if (n_exp <= 256) {
+    // G waves per token: all four for one token, two each for two, one each for more.
+#define KQ_SEL(PER)                                                                                 \
+  {                                                                                                 \
+    if (nt == 1) route_select_wg<PER, 4>(sel, logits, n_exp, top_k, t0, nt, top_idx, top_w);        \
+    else if (nt == 2) route_select_wg<PER, 2>(sel, logits, n_exp, top_k, t0, nt, top_idx, top_w);   \
+    else route_select_wg<PER, 1>(sel, logits, n_exp, top_k, t0, nt, top_idx, top_w);                \
+    return;                                                                                         \
+  }
+    if (n_exp <= 128) KQ_SEL(2)
+    KQ_SEL(4)
+#undef KQ_SEL
+  }
+  if (w >= nt) return;
   const int t = t0 + w;
   const float* lg = logits + (size_t)t * n_exp;
   int* ti = top_idx + (size_t)t * top_k;

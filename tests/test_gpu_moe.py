@@ -162,6 +162,8 @@ def test_moe_shared_gate_input_read_per_call(kinds):
 
 
 @pytest.mark.parametrize("T,n_exp,dim", [(1, 128, 2048), (8, 128, 2048), (32, 128, 2048), (203, 128, 2048),
+                                         (2, 128, 2048), (3, 64, 1024), (5, 200, 512),  # 2, 1 waves per token
+
                                          (400, 128, 2048), (522, 300, 1536),  # token-group router from 384 tokens
                                          (390, 64, 4096)])                    # dim above its limit: expert split
 def test_router_selection_matches_oracle(T, n_exp, dim):
@@ -199,6 +201,33 @@ def test_router_selection_matches_oracle(T, n_exp, dim):
                 gap = abs(float(ol[a]) - float(ol[b]))
                 assert gap <= err[a] + err[b] + 1e-30, \
                     f"token {t} rank {r}: GPU chose {a}, oracle {b}; logit gap {gap:.3e} > errors {err[a] + err[b]:.3e}"
+
+
+def test_router_nan_logit_follows_the_cpu_rule():
+    """A NaN router row makes every probability of the token NaN; the
+    selection then follows the greedy rule on the GPU's logits: no expert is
+    ever strictly greater, so every slot takes index 0, as the oracle's guard
+    does (the reference's Best_E stays 0 there and indexes Used (0), which
+    raises in Ada, llm_moe.adb:177-193, so no weight is pinned)."""
+    torch = torch_cuda()
+    dev = aa.DeviceOps()
+    gen = synth.rng(77)
+    n_exp, dim, top_k, T = 128, 512, 8, 6
+    W = (gen.standard_normal((n_exp, dim)) * 0.02).astype(np.float32)
+    W[5, 7] = np.nan
+    X = synth.activations_np(T * dim, gen).reshape(T, dim)
+    dW, dX = to_dev(W), to_dev(X)
+    logits = torch.empty((T, n_exp), dtype=torch.float32, device="cuda")
+    idx = torch.empty((T, top_k), dtype=torch.int32, device="cuda")
+    tw = torch.empty((T, top_k), dtype=torch.float32, device="cuda")
+    dev.route(dW.data_ptr(), n_exp, dim, T, top_k, dX.data_ptr(), logits.data_ptr(), idx.data_ptr(),
+              tw.data_ptr(), stream())
+    sync()
+    gl, gi = logits.cpu().numpy(), idx.cpu().numpy()
+    for t in range(T):
+        assert np.isnan(gl[t, 5])
+        oi, _ = oracle.route(gl[t], top_k)
+        assert gi[t].tolist() == oi.tolist() == [0] * top_k
 
 
 def test_router_ties_lowest_index():
