@@ -269,12 +269,18 @@ struct MvWorkspace {
 
 // Y[batch][out] = X W^T over packed W on `st`.  Batch 1 is the matvec.
 // Otherwise, by g_mm_engine: 0 picks, 1 forces the multi-vector VALU kernel,
-// 2 the 64-vector and 3 the 16-vector MFMA kernel where the kind has one.
-// The pick (measured on MI355X, Q4_K and Q6_K): up to 4 vectors on VALU;
-// 5-16 on the 16-vector kernel; beyond 16 the 64-vector kernel (one launch
-// for Q4_K; Q6_K launches of up to 32), except Q6_K on a matrix with at
-// least MM16_MIN_UNITS (64-row tile, super-block column) pairs, which runs
-// the 16-vector kernel in launches of 16.
+// 2 the 64-vector and 3 the 16-vector MFMA kernel, 4 the one-pass kernel
+// (kq_mmv.hip) and 5 the batch-1 kernel for up to 4 vectors per launch,
+// where the kind has one.
+// The pick for Q4_K and Q6_K (measured on MI355X at 4096x4096 and
+// 14336x4096, `small_batch` of bench.py):
+//   up to 4 vectors: the batch-1 kernel on 4 vectors (Q6_K; Q4_K where its
+//     batch-1 plan is 16-row workgroups), else one-pass above 2 vectors and
+//     the VALU kernel at 2;
+//   5-16 vectors: one pass;
+//   above 16: one pass for Q6_K; Q4_K on the 64-vector kernel in one launch,
+//     or the 16-vector one on matrices of at least MM16_MIN_UNITS (64-row
+//     tile, super-block column) pairs.
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;
@@ -300,6 +306,16 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   // Q6_K in launches of at most 32 vectors: the 64-vector kernel's Q6_K
   // variant runs out of registers above 32 (14336x4096: 359 us for 64
   // vectors in one launch, 82 us per 32).
+  if (eng == 4 && kq::mmv_kind(kind)) return {3, 64};
+  if (eng == 5 && kq::matvec_nv_takes(kind, in_dim, out_dim)) return {4, 4};
+  if (eng == 0 && kq::mmv_kind(kind) && kq::matvec_nv_takes(kind, in_dim, out_dim)) {
+    if (batch <= 4) {
+      if (kind == kq::Q6_K || kq::mfma_plan(kind, in_dim, out_dim).blk16) return {4, 4};
+      if (batch > 2) return {3, 64};
+      return {0, MULTI_MAX_BATCH};
+    }
+    if (batch <= 16 || kind == kq::Q6_K) return {3, 64};
+  }
   if (mm16) return {1, 16};
   if (mm64) return {2, kind == kq::Q6_K ? 32 : 64};
   return {0, MULTI_MAX_BATCH};
@@ -310,7 +326,7 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
 size_t mm_launch_need(int kind, int in_dim, int out_dim, int batch) {
   if (batch <= 1) return 0;
   const MmRoute r = mm_route(kind, in_dim, out_dim, batch);
-  if (r.family == 0) return 0;
+  if (r.family == 0 || r.family >= 3) return 0;
   if (r.family == 1) return kq::mm16_workspace_bytes(in_dim, out_dim);
   size_t n = kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, r.step));
   if (batch > r.step && batch % r.step) n = std::max(n, kq::mfma_workspace_bytes(in_dim, out_dim, batch % r.step));
@@ -327,7 +343,11 @@ hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int b
     const float* xb = X + (size_t)b0 * in_dim;
     float* yb = Y + (size_t)b0 * out_dim;
     hipError_t e;
-    if (r.family == 1)
+    if (r.family == 4)
+      e = kq::launch_matvec_mfma_nv(kind, P, in_dim, out_dim, nb, xb, yb, st);
+    else if (r.family == 3)
+      e = kq::launch_matmul_mmv(kind, P, in_dim, out_dim, nb, xb, yb, st);
+    else if (r.family == 1)
       e = kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st, batch <= r.step);
     else if (r.family == 2)
       e = kq::launch_matmul_mfma_packed(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st,
@@ -1083,7 +1103,7 @@ extern "C" int aspida_kq_set_mv_engine(int engine) {
 }
 
 extern "C" int aspida_kq_set_mm_engine(int engine) {
-  if (engine < 0 || engine > 3) return -EINVAL;
+  if (engine < 0 || engine > 5) return -EINVAL;
   g_mm_engine.store(engine, std::memory_order_relaxed);
   return 0;
 }

@@ -91,6 +91,18 @@ hipError_t launch_matmul_mfma_packed(int kind, const void* P, int in_dim, int ou
 // Up to 16 activation rows per launch on MFMA, dense in rows and vectors
 // (kq_mm16.hip): kinds it takes, workspace bytes (activation images and
 // partials), and the launcher; `count` as above.
+// Up to 4 vectors with the batch-1 matrix-core arithmetic on 16-row
+// workgroups, each column's weights read once for all of them
+// (kq_mv_mfma.hip); Q4_K and Q6_K (matvec_nv_takes).
+bool matvec_nv_takes(int kind, int in_dim, int out_dim);
+hipError_t launch_matvec_mfma_nv(int kind, const void* P, int in_dim, int out_dim, int nv, const float* x, float* y,
+                                 hipStream_t s);
+// Small batches of 2..64 vectors over packed Q4_K / Q6_K on the matrix
+// cores with the batch-1 work split (kq_mmv.hip): every weight byte read once,
+// no workspace, no pre-pass.  x must be 16-byte aligned.
+bool mmv_kind(int kind);
+hipError_t launch_matmul_mmv(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
+                             hipStream_t s);
 bool mm16_kind(int kind);
 size_t mm16_workspace_bytes(int in_dim, int out_dim);
 hipError_t launch_matmul_mm16(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,

@@ -683,4 +683,64 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
   return ((rr[0] + rr[16]) + rr[32]) + rr[48];
 }
 
+__device__ __forceinline__ float4 ld_f4(const float* p) {
+  float4 v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(p, 16), 16);
+  return v;
+}
+
+// NV vectors x_v = x + v ldx at once (rows v >= nv repeat vector nv - 1;
+// the caller does not write them): each column's weights are loaded once,
+// then every vector gets its activation image and the column's MFMA dot
+// (mv_column) against them, with the same arithmetic as mv_mfma_rows.  The
+// columns are taken one after another.  out[v] is row `lane` (RB = 4) or
+// row 16 rb0 + lane % 16 (RB = 1) of vector v.
+template <int KIND, int RB, int NV>
+__device__ __forceinline__ void mv_mfma_rows_nv(const uint8_t* __restrict__ P, int nsb, int tile, int sb0, int spw,
+                                                const float* __restrict__ x, size_t ldx, int nv,
+                                                uint4 (&img)[8][RB == 4 ? 64 : 17], float* xsum, MvHdr<KIND>* hdr,
+                                                int lane, int rb0, float (&out)[NV]) {
+  constexpr int GB = 64 * Block<KIND>::BYTES;
+  const uint8_t* gp = P + ((size_t)tile * nsb + sb0) * GB;
+  const float* xp[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) xp[v] = x + (size_t)(v < nv ? v : nv - 1) * ldx + (size_t)sb0 * 256 + 4 * lane;
+  MvCol<KIND, RB> c0;
+  float4 xv[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) xv[v] = ld_f4(xp[v]);
+  c0.load(gp, lane, rb0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (RB == 4 || lane < 17) img[j][lane] = make_uint4(0u, 0u, 0u, 0u);
+  const MvLane L = mv_lane<KIND>(img, lane);
+  float acc[NV][RB];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[v][rb] = 0.f;
+  for (int s = 0; s < spw; ++s) {
+    if (s > 0) {
+      asm volatile("" ::: "memory");  // the next column's loads stay after this column's work
+#pragma unroll
+      for (int v = 0; v < NV; ++v) xv[v] = ld_f4(xp[v] + (size_t)s * 256);
+      c0.load(gp + (size_t)s * GB, lane, rb0);
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) mv_column(c0, xv[v], L, img, xsum, hdr, lane, acc[v]);
+  }
+  // Lane (n, g) holds rows 16 rb + n over its quarter: add the four quarters
+  // (ascending g), vector by vector.
+  float* red = reinterpret_cast<float*>(&img[0][0]);
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) red[rb * 64 + lane] = acc[v][rb];
+    __builtin_amdgcn_wave_barrier();
+    const float* rr = red + (RB == 4 ? (lane >> 4) * 64 : 0) + (lane & 15);
+    out[v] = ((rr[0] + rr[16]) + rr[32]) + rr[48];
+  }
+}
+
 }  // namespace kq

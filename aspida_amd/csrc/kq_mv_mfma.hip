@@ -149,6 +149,37 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma2_16(const uint8_t* __restr
   }
 }
 
+// Small batches of NV <= 4 vectors with the batch-1 arithmetic: each
+// column's weights are read once for every vector (mv_mfma_rows_nv), on
+// 16-row workgroups as kq_mv_mfma16 (on 64-row ones the vectors' registers
+// do not fit 16 waves).  Y[v][out_rows] for v < nv.
+template <int KIND, int NW, int NV>
+__global__ __launch_bounds__(64 * NW) void kq_mv_mfma16n(const uint8_t* __restrict__ P, int nsb, int out_rows,
+                                                        const float* __restrict__ x, float* __restrict__ y, int spw,
+                                                        int nv) {
+  __shared__ MvShared16 sh[NW];
+  __shared__ float red16[NW][NV][16];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = blockIdx.x;
+  float r[NV];
+  mv_mfma_rows_nv<KIND, 1, NV>(P, nsb, blk >> 2, w * spw, spw, x, (size_t)nsb * 256, nv, sh[w].img, sh[w].xsum,
+                               (MvHdr<KIND>*)nullptr, lane, blk & 3, r);
+  if (lane < 16)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) red16[w][v][lane] = r[v];
+  __syncthreads();
+  if (w != 0 || lane >= 16) return;
+  const int row = 16 * blk + lane;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float t = red16[0][v][lane];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) t += red16[k][v][lane];
+    if (v < nv && row < out_rows) y[(size_t)v * out_rows + row] = t;
+  }
+}
+
 // 0: the MFMA kernel for Q4_K and Q6_K, 1: the VALU kernel (comparison and tuning).
 static std::atomic<int> g_engine{0};
 
@@ -340,6 +371,49 @@ hipError_t launch_matvec2_mfma(int kind_a, const void* Pa, int out_a, float* ya,
   if (kind_a == Q4_K && kind_b == Q4_K) return launch_mfma_pair<Q4_K, Q4_K>(a, out_a, ya, b, out_b, yb, in_dim, x, part, count, s);
   if (kind_a == Q6_K && kind_b == Q6_K) return launch_mfma_pair<Q6_K, Q6_K>(a, out_a, ya, b, out_b, yb, in_dim, x, part, count, s);
   if (kind_a == Q6_K && kind_b == Q4_K) return launch_mfma_pair<Q6_K, Q4_K>(a, out_a, ya, b, out_b, yb, in_dim, x, part, count, s);
+  return hipErrorNotSupported;
+}
+
+// Waves per 16-row workgroup: the most of 16, 14, 8, 4, 2, 1 dividing the
+// columns; each takes its columns one after another.
+template <int KIND, int NV>
+static hipError_t launch_mfma_nv_kind(const uint8_t* w, int in_dim, int out_dim, int nv, const float* x, float* y,
+                                      hipStream_t s) {
+  const int nsb = in_dim / 256;
+  int nw = 1;
+  for (int c : {16, 14, 8, 4, 2})
+    if (nsb % c == 0) {
+      nw = c;
+      break;
+    }
+  const int spw = nsb / nw;
+  const dim3 grid((out_dim + 15) / 16);
+#define KQ_GO(N)                                                                                                 \
+  case N:                                                                                                        \
+    hipLaunchKernelGGL((kq_mv_mfma16n<KIND, N, NV>), grid, dim3(64 * N),                                         \
+                       mv16_spread_lds((int)grid.x, lds_room<kq_mv_mfma16n<KIND, N, NV>, N>()), s, w, nsb, out_dim, x, \
+                       y, spw, nv);                                                                              \
+    break;
+  switch (nw) {
+    KQ_GO(16) KQ_GO(14) KQ_GO(8) KQ_GO(4) KQ_GO(2) KQ_GO(1)
+    default: return hipErrorInvalidValue;
+  }
+#undef KQ_GO
+  return hipGetLastError();
+}
+
+bool matvec_nv_takes(int kind, int in_dim, int out_dim) {
+  return (kind == Q4_K || kind == Q6_K) && in_dim > 0 && in_dim % 256 == 0 && out_dim > 0;
+}
+
+hipError_t launch_matvec_mfma_nv(int kind, const void* P, int in_dim, int out_dim, int nv, const float* x, float* y,
+                                 hipStream_t s) {
+  const uint8_t* w = (const uint8_t*)P;
+  if (nv < 1 || nv > 4) return hipErrorInvalidValue;
+  if (kind == Q4_K) return nv <= 2 ? launch_mfma_nv_kind<Q4_K, 2>(w, in_dim, out_dim, nv, x, y, s)
+                                   : launch_mfma_nv_kind<Q4_K, 4>(w, in_dim, out_dim, nv, x, y, s);
+  if (kind == Q6_K) return nv <= 2 ? launch_mfma_nv_kind<Q6_K, 2>(w, in_dim, out_dim, nv, x, y, s)
+                                   : launch_mfma_nv_kind<Q6_K, 4>(w, in_dim, out_dim, nv, x, y, s);
   return hipErrorNotSupported;
 }
 

@@ -300,9 +300,9 @@ def kquant_table(torch, aa, synth, seed, stream):
 
 def small_batch_table(torch, aa, synth, seed, stream):
     """Small-batch products: Q4_K and Q6_K at 4096x4096 and
-    14336x4096 for B in {2, 4, 8, 16, 32, 64}, packed weights (the
-    multi-vector VALU kernel up to B = 4, MFMA above), launches rotating over
-    >= 1 GiB of weight copies.  GB/s counts W + 4 B (in + out) bytes;
+    14336x4096 for B in {2, 4, 8, 16, 32, 64}, packed weights (the library's
+    pick per kind, shape and batch: small_batch_kernel), launches rotating
+    over >= 1 GiB of weight copies.  GB/s counts W + 4 B (in + out) bytes;
     TFLOP/s counts 2 B in out."""
     dev = aa.DeviceOps()
     g = torch.Generator(device="cuda")
@@ -353,14 +353,22 @@ def small_batch_table(torch, aa, synth, seed, stream):
 
 
 def small_batch_kernel(aa, kind, inp, out, B):
-    """The kernel the library's default small-batch pick runs (matmul_packed in
-    aspidagpu.hip): the multi-vector VALU kernel up to 4 vectors; then the
-    16-vector MFMA kernel (above 16 vectors only for matrices of >= 2048
-    64-row-by-256-column blocks), else the 64-vector MFMA kernel."""
+    """The kernel the library's default small-batch pick runs (mm_route in
+    aspidagpu.hip) for Q4_K and Q6_K: up to 4 vectors the batch-1 kernel on
+    4 vectors (Q6_K, and Q4_K where the batch-1 plan is 16-row workgroups;
+    else the vector kernel at 2 and the one-pass kernel at 3-4); the one-pass
+    kernel up to 16 vectors and for Q6_K above; Q4_K above 16 on the
+    16-vector MFMA kernel for matrices of >= 2048 64-row-by-256-column blocks,
+    else the 64-vector one."""
     if B <= 4:
-        return "kq_mm_packed_valu"
-    if B <= 16 or (-(-out // 64)) * (inp // 256) >= 2048:
-        return "kq_mm16_q4k" if kind == aa.Q4_K else "kq_mm16_q6k"
+        b16 = aa.DeviceOps().matvec_plan(kind, inp, out)[5]
+        if kind == aa.Q6_K or b16:
+            return "kq_mv_mfma16n"
+        return "kq_mmv" if B > 2 else "kq_mm_packed_valu"
+    if B <= 16 or kind == aa.Q6_K:
+        return "kq_mmv"
+    if (-(-out // 64)) * (inp // 256) >= 2048:
+        return "kq_mm16_q4k"
     return "kq_mm_mfma"
 
 

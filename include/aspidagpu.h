@@ -408,12 +408,17 @@ int aspida_kq_set_mv_engine(int engine);
 
 /* Engine of the packed small-batch product (batch > 1 in
  * aspida_kq_matmul_packed_dev and aspida_gpu_matmul): 0 = the built-in choice
- * (Q4_K and Q6_K up to 4 vectors on the vector kernel, then Q4_K on the
- * 16-vector matrix-core kernel -- above 16 vectors only for matrices of at
- * least 2048 64-row-by-256-column blocks, else the 64-vector one -- and Q6_K
- * on the 64-vector matrix-core kernel; other kinds on the vector kernel); 1 = the
- * vector kernel; 2 = the 64-vector and 3 = the 16-vector matrix-core kernel
- * for the kinds that have one (others stay on the vector kernel).
+ * (Q4_K and Q6_K: up to 4 vectors on the batch-1 matrix-core kernel -- Q4_K
+ * matrices whose batch-1 plan is 64-row workgroups take the vector kernel at
+ * 2 vectors and the one-pass kernel at 3-4 -- then the one-pass kernel up to
+ * 16 vectors; above 16 the one-pass kernel for Q6_K, and for Q4_K the
+ * 16-vector matrix-core kernel on matrices of at least 2048
+ * 64-row-by-256-column blocks, else the 64-vector one; other kinds on the
+ * vector kernel); 1 = the vector kernel; 2 = the 64-vector and 3 = the
+ * 16-vector matrix-core kernel; 4 = the one-pass matrix-core kernel (up to
+ * 64 vectors per weight pass); 5 = the batch-1 matrix-core kernel on up to 4
+ * vectors per launch; for the kinds that have one (others stay on the
+ * vector kernel).
  * Process-wide; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mm_engine(int engine);

@@ -185,12 +185,21 @@ def test_matmul_workspace_covers_every_launch(lib):
 
 def test_matmul_workspace_advisor_shapes(lib):
     """The shapes where a 64-row padding undersized the buffer: Q6_K
-    8960->1536 at B=48 and Q4_K/Q6_K 3584x3584 at B=48 and 65."""
-    for kind, in_dim, out_dim, batch in [(aa.Q6_K, 8960, 1536, 48), (aa.Q4_K, 3584, 3584, 48),
-                                         (aa.Q6_K, 3584, 3584, 48), (aa.Q4_K, 3584, 3584, 65),
-                                         (aa.Q6_K, 3584, 3584, 65)]:
+    8960->1536 at B=48 and Q4_K/Q6_K 3584x3584 at B=48 and 65 -- on the
+    64-vector kernel (engine 2), whose launches need the workspace, and on the
+    built-in pick (Q6_K there runs the one-pass kernel, which needs none)."""
+    cases = [(aa.Q6_K, 8960, 1536, 48), (aa.Q4_K, 3584, 3584, 48), (aa.Q6_K, 3584, 3584, 48),
+             (aa.Q4_K, 3584, 3584, 65), (aa.Q6_K, 3584, 3584, 65)]
+    assert lib.aspida_kq_set_mm_engine(2) == 0
+    try:
+        for kind, in_dim, out_dim, batch in cases:
+            alloc, need = _matmul_ws(lib, kind, in_dim, out_dim, batch)
+            assert need > 0 and alloc >= need, (kind, in_dim, out_dim, batch, alloc, need)
+    finally:
+        assert lib.aspida_kq_set_mm_engine(0) == 0
+    for kind, in_dim, out_dim, batch in cases:
         alloc, need = _matmul_ws(lib, kind, in_dim, out_dim, batch)
-        assert need > 0 and alloc >= need, (kind, in_dim, out_dim, batch, alloc, need)
+        assert alloc >= need, (kind, in_dim, out_dim, batch, alloc, need)
 
 
 def test_chain_abi_rejects_without_a_model(lib):

@@ -175,10 +175,13 @@ def test_mfma_matmul_matches_oracle(kind, case):
 # at and above 16 (two 16-vector launches, one ragged), ragged weight rows,
 # one column per wave and long column runs, tiles split over workgroups.
 MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304), (40, 4096, 4096),
-                   (9, 16448, 2048), (3, 256, 14336)]
+                   (9, 16448, 2048), (3, 256, 14336), (20, 12352, 512), (64, 12352, 256), (63, 300, 1024)]
 
 
-@pytest.mark.parametrize("engine", [1, 2, 3])
+# Engine 4 is the one-pass kernel (kq_mmv.hip): 64-row tiles from 12352 rows
+# (193 tiles), 16-row blocks below; up to 64 vectors in one launch.  Engine 5
+# runs up to 4 vectors per launch on the batch-1 16-row kernels.
+@pytest.mark.parametrize("engine", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("case", MM_ENGINE_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
 def test_mm_engines_match_oracle(kind, case, engine):
@@ -197,8 +200,18 @@ def test_mm_engines_match_oracle(kind, case, engine):
                         what=f"engine {engine} B={batch} {out_dim}x{in_dim}")
 
 
+def _engine_matmul(engine, kind, w, X, in_dim, out_dim):
+    dev = aa.DeviceOps()
+    dev.set_mm_engine(engine)
+    try:
+        return _packed_matmul(kind, w, X, in_dim, out_dim)
+    finally:
+        dev.set_mm_engine(0)
+
+
+@pytest.mark.parametrize("engine", [0, 4, 5])
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K])
-def test_mfma_matmul_row_scales(kind):
+def test_mfma_matmul_row_scales(kind, engine):
     """Activation rows spanning 1e-30..1e30 in magnitude (each row is split
     with its own power-of-two scale) and an all-zero row."""
     gen = synth.rng(77 + kind)
@@ -207,22 +220,23 @@ def test_mfma_matmul_row_scales(kind):
     X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
     X *= (10.0 ** np.array([-30, -12, -3, 0, 0, 3, 12, 30, 0]))[:, None].astype(np.float32)
     X[8] = 0.0
-    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    Y = _engine_matmul(engine, kind, w, X, in_dim, out_dim)
     want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
     assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
                         what=f"{aa.KIND_NAMES[kind]} scaled rows")
     assert np.all(Y[8] == 0.0)
 
 
+@pytest.mark.parametrize("engine", [0, 4, 5])
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K])
-def test_mfma_matmul_special_scales(kind):
+def test_mfma_matmul_special_scales(kind, engine):
     """Raw random bytes everywhere: f16 scales include +-0, subnormals, Inf and
     NaN, which Aspida reads as +0.0."""
     gen = synth.rng(88 + kind)
     batch, out_dim, in_dim = 4, 64, 1024
     w = gen.integers(0, 256, aa.weight_bytes(kind, in_dim, out_dim), dtype=np.uint8)
     X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
-    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    Y = _engine_matmul(engine, kind, w, X, in_dim, out_dim)
     want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
     assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
                         what=f"{aa.KIND_NAMES[kind]} specials")
