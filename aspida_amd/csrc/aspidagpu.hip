@@ -310,9 +310,8 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   if (eng == 5 && kq::matvec_nv_takes(kind, in_dim, out_dim)) return {4, 4};
   if (eng == 0 && kq::mmv_kind(kind) && kq::matvec_nv_takes(kind, in_dim, out_dim)) {
     if (batch <= 4) {
-      if (kind == kq::Q6_K || kq::mfma_plan(kind, in_dim, out_dim).blk16) return {4, 4};
-      if (batch > 2) return {3, 64};
-      return {0, MULTI_MAX_BATCH};
+      if (kq::mfma_plan(kind, in_dim, out_dim).blk16 || (kind == kq::Q6_K && batch <= 2)) return {4, 4};
+      return {3, 64};
     }
     if (batch <= 16 || kind == kq::Q6_K) return {3, 64};
   }

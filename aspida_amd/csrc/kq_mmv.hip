@@ -161,6 +161,100 @@ template <> struct MmvX<Q6_K> {
   }
 };
 
+// Staged conversion of a group of GV <= 4 vectors (GV = 8 also works): lane l converts vector
+// v0 + l / (64 / GV), elements E c .. E c + E - 1 (E = 4 GV, c = l % (64 / GV))
+// -- every lane busy, E elements each instead of 64 -- into the wave's LDS
+// planes in A order (position 8 m + j holds element 8 m + ord[j], ord =
+// 0 2 1 3 4 6 5 7, the pair order of the codes), then each lane reads its A
+// operands (rows b >= GV are zero).  Same scale S per (vector, column), the
+// same hi / lo split and, for Q4_K, the same sub-block sums as the direct
+// build above.
+// A vector's planes are 33 chunks of 16 bytes apart, so the 16 vectors a
+// quarter-wave reads sit in distinct banks.
+template <int GV>
+struct MmvStage {
+  uint4 hi[GV][33], lo[GV][33];  // 256 f16 per vector and plane (+ 1 pad)
+  float sum[GV][8];              // sub-block sums of x S (Q4_K)
+  float inv[16];                 // 1/S per vector of the group (zero past GV)
+};
+
+template <int LPV>
+__device__ __forceinline__ float mmv_group_max(float v) {
+#pragma unroll
+  for (int o = 1; o < LPV; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+template <int KIND, int GV>
+__device__ __forceinline__ void mmv_build_staged(MmvX<KIND>& A, MmvStage<GV>& st, const float* __restrict__ X,
+                                                 int in_dim, int B, int v0, int col, int lane) {
+  constexpr int LPV = 64 / GV, E = 4 * GV;
+  const int vw = lane / LPV, c = lane % LPV, v = v0 + vw;
+  float4 x[E / 4];
+  const float4* p = reinterpret_cast<const float4*>(X + (size_t)(v < B ? v : 0) * in_dim + (size_t)col * 256 + E * c);
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i) x[i] = v < B ? p[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i) mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x[i].x), fabsf(x[i].y)), fmaxf(fabsf(x[i].z), fabsf(x[i].w))));
+  mx = mmv_group_max<LPV>(mx);
+  int e = 0;
+  const bool scaled = mx > 0.f && __builtin_isfinite(mx);
+  if (scaled) (void)frexpf(mx, &e);
+  const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
+  const float S = ldexpf(1.f, se), S11 = ldexpf(1.f, se + 11);
+  float su = 0.f;
+#pragma unroll
+  for (int k = 0; k < E / 8; ++k) {
+    const float4 a = x[2 * k], b = x[2 * k + 1];
+    uint32_t h0, l0, h1, l1, h2, l2, h3, l3;
+    mmv_split(a.x, a.z, S, S11, h0, l0);  // elements 0, 2
+    mmv_split(a.y, a.w, S, S11, h1, l1);  // 1, 3
+    mmv_split(b.x, b.z, S, S11, h2, l2);  // 4, 6
+    mmv_split(b.y, b.w, S, S11, h3, l3);  // 5, 7
+    st.hi[vw][E / 8 * c + k] = make_uint4(h0, h1, h2, h3);
+    st.lo[vw][E / 8 * c + k] = make_uint4(l0, l1, l2, l3);
+    if constexpr (KIND == Q4_K) su += (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) * S;
+  }
+  if constexpr (KIND == Q4_K) {
+    // Sub-block t = elements 32 t .. + 31: 32 / E lanes of the vector.
+#pragma unroll
+    for (int o = 1; o < 32 / E; o <<= 1) su += __shfl_xor(su, o, 64);
+    if (c % (32 / E) == 0) st.sum[vw][c / (32 / E)] = su;
+  }
+  if (c == 0) st.inv[vw] = ldexpf(1.f, -se);
+  if (lane >= GV && lane < 16) st.inv[lane] = 0.f;
+  __builtin_amdgcn_wave_barrier();
+  const int b = lane & 15, kg = lane >> 4;
+  const bool has = b < GV;
+  const int bb = has ? b : 0;
+  if constexpr (KIND == Q4_K) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint4 h = st.hi[bb][4 * t + kg], l = st.lo[bb][4 * t + kg];
+      A.ah[t] = has ? h : make_uint4(0u, 0u, 0u, 0u);
+      A.al[t] = has ? l : make_uint4(0u, 0u, 0u, 0u);
+    }
+    const int t0 = 4 * (kg & 1);
+    _Float16 h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float u = has && kg < 2 ? st.sum[bb][t0 + i] * MMV_XSUM : 0.f;
+      h[i] = (_Float16)u;
+      l[i] = (_Float16)((u - (float)h[i]) * 2048.f);
+    }
+    A.as = make_uint4(pack_f16x2(h[0], h[1]), pack_f16x2(h[2], h[3]), pack_f16x2(l[0], l[1]), pack_f16x2(l[2], l[3]));
+  } else {
+    const uint2* h2 = reinterpret_cast<const uint2*>(&st.hi[bb][0]);
+    const uint2* l2 = reinterpret_cast<const uint2*>(&st.lo[bb][0]);
+#pragma unroll
+    for (int sb = 0; sb < 16; ++sb) {
+      const uint2 h = h2[4 * sb + kg], l = l2[4 * sb + kg];
+      A.a6[sb] = has ? make_uint4(h.x, h.y, l.x, l.y) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+}
+
 // One 16-row block's weights of a column as lane (n, kg) loads them (row r =
 // 16 rbb + n of the 64-row group at grp).
 template <int KIND> struct MmvW;
@@ -273,13 +367,18 @@ __device__ __forceinline__ void mmv_dot(const MmvW<Q6_K>& W, const MmvX<Q6_K>& A
 
 // Workgroup: RB 16-row blocks (RB = 1: block blockIdx.x, block b % 4 of
 // tile b / 4; RB = 4: tile blockIdx.x) over every column, NW waves each
-// taking columns w spw .. + spw - 1 one after another, NG groups of 16
-// vectors per column (weights loaded once for all of them).
-template <int KIND, int RB, int NW, int NG>
+// taking columns w spw .. + spw - 1 one after another, NG groups of GV
+// vectors per column (weights loaded once for all of them).  GV = 16 builds
+// the A operands directly in registers; GV = 2 and 4 (batches of up to 4 on
+// at most 8 waves) stage them through LDS: measured on MI355X, 14336x4096
+// at 2 vectors 15.2 -> 12.5 us (Q4_K), 4 vectors 27.6 -> 19.9 us (Q6_K);
+// at 8 vectors the staged build was slower than the direct one.
+template <int KIND, int RB, int NW, int NG, int GV>
 __global__ __launch_bounds__(64 * NW) void kq_mmv(MmvArgs a) {
   constexpr int GB = 64 * Block<KIND>::BYTES;
   __shared__ float red[NW][256];
   __shared__ float sinv[NW][16];
+  __shared__ MmvStage<GV < 16 ? GV : 1> stage[GV < 16 ? NW : 1];
   const int lane = threadIdx.x & 63, q = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = RB == 4 ? blockIdx.x : blockIdx.x >> 2, rb0 = RB == 4 ? 0 : blockIdx.x & 3;
@@ -300,13 +399,19 @@ __global__ __launch_bounds__(64 * NW) void kq_mmv(MmvArgs a) {
     for (int rb = 0; rb < RB; ++rb) W[rb].load(grp, rb0 + rb, lane);
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      if (16 * g < a.B) {
+      if (GV * g < a.B) {
         MmvX<KIND> A;
-        const float inv = A.build(a.X, in_dim, a.B, 16 * g, col, lane);
+        float4 iv;
         __builtin_amdgcn_wave_barrier();
-        if (lane < 16) sinv[w][lane] = inv;
-        __builtin_amdgcn_wave_barrier();
-        const float4 iv = *reinterpret_cast<const float4*>(&sinv[w][4 * q]);
+        if constexpr (GV < 16) {
+          mmv_build_staged<KIND, GV>(A, stage[w], a.X, in_dim, a.B, GV * g, col, lane);
+          iv = *reinterpret_cast<const float4*>(&stage[w].inv[4 * q]);
+        } else {
+          const float inv = A.build(a.X, in_dim, a.B, 16 * g, col, lane);
+          if (lane < 16) sinv[w][lane] = inv;
+          __builtin_amdgcn_wave_barrier();
+          iv = *reinterpret_cast<const float4*>(&sinv[w][4 * q]);
+        }
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) mmv_dot(W[rb], A, iv, acc[rb][g]);
@@ -314,12 +419,12 @@ __global__ __launch_bounds__(64 * NW) void kq_mmv(MmvArgs a) {
     }
   }
   // The waves' sums, ascending w: per (block, group), thread t < 256 owns
-  // vector 16 g + 4 (t % 64 / 16) + t / 64 of row t % 16 of the block.
+  // vector GV g + 4 (t % 64 / 16) + t / 64 of row t % 16 of the block.
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      if (16 * g >= a.B) continue;
+      if (GV * g >= a.B) continue;
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[w][i * 64 + lane] = acc[rb][g][i];
       __syncthreads();
@@ -327,9 +432,9 @@ __global__ __launch_bounds__(64 * NW) void kq_mmv(MmvArgs a) {
         float sum = red[0][t];
 #pragma unroll
         for (int k = 1; k < NW; ++k) sum += red[k][t];
-        const int l = t & 63, v = 16 * g + 4 * (l >> 4) + (t >> 6);
+        const int l = t & 63, vi = 4 * (l >> 4) + (t >> 6), v = GV * g + vi;
         const int row = tile * 64 + 16 * (rb0 + rb) + (l & 15);
-        if (v < a.B && row < a.out_rows) a.Y[(size_t)v * a.out_rows + row] = sum;
+        if (vi < GV && v < a.B && row < a.out_rows) a.Y[(size_t)v * a.out_rows + row] = sum;
       }
       __syncthreads();
     }
@@ -387,14 +492,16 @@ hipError_t launch_matmul_mmv(int kind, const void* P, int in_dim, int out_dim, i
     p.spw *= 2;
   }
   const MmvArgs a{(const uint8_t*)P, in_dim / 256, out_dim, batch, p.spw, X, Y};
-#define KQ_MMV(K, RB, NW, NG) hipLaunchKernelGGL((kq_mmv<K, RB, NW, NG>), grid, dim3(64 * NW), 0, s, a)
-#define KQ_MMV_NG(K, RB, NW)              \
-  switch (ng) {                           \
-    case 1: KQ_MMV(K, RB, NW, 1); break;  \
-    case 2: KQ_MMV(K, RB, NW, 2); break;  \
-    case 3: KQ_MMV(K, RB, NW, 3); break;  \
-    default: KQ_MMV(K, RB, NW, 4); break; \
-  }
+#define KQ_MMV(K, RB, NW, NG, GV) hipLaunchKernelGGL((kq_mmv<K, RB, NW, NG, GV>), grid, dim3(64 * NW), 0, s, a)
+#define KQ_MMV_NG(K, RB, NW)                    \
+  if (batch <= 2) KQ_MMV(K, RB, NW, 1, 2);      \
+  else if (batch <= 4) KQ_MMV(K, RB, NW, 1, 4); \
+  else switch (ng) {                            \
+      case 1: KQ_MMV(K, RB, NW, 1, 16); break;  \
+      case 2: KQ_MMV(K, RB, NW, 2, 16); break;  \
+      case 3: KQ_MMV(K, RB, NW, 3, 16); break;  \
+      default: KQ_MMV(K, RB, NW, 4, 16); break; \
+    }
 #define KQ_MMV_NW(K, RB)                             \
   switch (p.nw) {                                    \
     case 8: KQ_MMV_NG(K, RB, 8) break;               \
@@ -403,7 +510,7 @@ hipError_t launch_matmul_mmv(int kind, const void* P, int in_dim, int out_dim, i
     default: KQ_MMV_NG(K, RB, 1) break;              \
   }
   if (kind == Q4_K) {
-    if (p.nw == 16) KQ_MMV(Q4_K, 1, 16, 1);
+    if (p.nw == 16) KQ_MMV(Q4_K, 1, 16, 1, 16);
     else if (p.rb == 4) KQ_MMV_NW(Q4_K, 4) else KQ_MMV_NW(Q4_K, 1)
   } else {
     if (p.rb == 4) KQ_MMV_NW(Q6_K, 4) else KQ_MMV_NW(Q6_K, 1)

@@ -355,16 +355,14 @@ def small_batch_table(torch, aa, synth, seed, stream):
 def small_batch_kernel(aa, kind, inp, out, B):
     """The kernel the library's default small-batch pick runs (mm_route in
     aspidagpu.hip) for Q4_K and Q6_K: up to 4 vectors the batch-1 kernel on
-    4 vectors (Q6_K, and Q4_K where the batch-1 plan is 16-row workgroups;
-    else the vector kernel at 2 and the one-pass kernel at 3-4); the one-pass
-    kernel up to 16 vectors and for Q6_K above; Q4_K above 16 on the
+    4 vectors where the batch-1 plan is 16-row workgroups (and Q6_K at 2),
+    else the one-pass kernel; the one-pass kernel up to 16 vectors and for
+    Q6_K above; Q4_K above 16 on the
     16-vector MFMA kernel for matrices of >= 2048 64-row-by-256-column blocks,
     else the 64-vector one."""
     if B <= 4:
         b16 = aa.DeviceOps().matvec_plan(kind, inp, out)[5]
-        if kind == aa.Q6_K or b16:
-            return "kq_mv_mfma16n"
-        return "kq_mmv" if B > 2 else "kq_mm_packed_valu"
+        return "kq_mv_mfma16n" if b16 or (kind == aa.Q6_K and B <= 2) else "kq_mmv"
     if B <= 16 or kind == aa.Q6_K:
         return "kq_mmv"
     if (-(-out // 64)) * (inp // 256) >= 2048:

@@ -408,9 +408,9 @@ int aspida_kq_set_mv_engine(int engine);
 
 /* Engine of the packed small-batch product (batch > 1 in
  * aspida_kq_matmul_packed_dev and aspida_gpu_matmul): 0 = the built-in choice
- * (Q4_K and Q6_K: up to 4 vectors on the batch-1 matrix-core kernel -- Q4_K
- * matrices whose batch-1 plan is 64-row workgroups take the vector kernel at
- * 2 vectors and the one-pass kernel at 3-4 -- then the one-pass kernel up to
+ * (Q4_K and Q6_K: up to 4 vectors on the batch-1 matrix-core kernel where
+ * the batch-1 plan is 16-row workgroups, else the one-pass kernel -- Q6_K
+ * keeps the batch-1 kernel at 2 vectors -- then the one-pass kernel up to
  * 16 vectors; above 16 the one-pass kernel for Q6_K, and for Q4_K the
  * 16-vector matrix-core kernel on matrices of at least 2048
  * 64-row-by-256-column blocks, else the 64-vector one; other kinds on the

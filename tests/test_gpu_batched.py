@@ -175,11 +175,13 @@ def test_mfma_matmul_matches_oracle(kind, case):
 # at and above 16 (two 16-vector launches, one ragged), ragged weight rows,
 # one column per wave and long column runs, tiles split over workgroups.
 MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304), (40, 4096, 4096),
-                   (9, 16448, 2048), (3, 256, 14336), (20, 12352, 512), (64, 12352, 256), (63, 300, 1024)]
+                   (9, 16448, 2048), (3, 256, 14336), (20, 12352, 512), (64, 12352, 256), (63, 300, 1024),
+                   (2, 13000, 256), (4, 12352, 512)]
 
 
 # Engine 4 is the one-pass kernel (kq_mmv.hip): 64-row tiles from 12352 rows
-# (193 tiles), 16-row blocks below; up to 64 vectors in one launch.  Engine 5
+# (193 tiles), 16-row blocks below; up to 64 vectors in one launch, up to 4
+# converted through LDS.  Engine 5
 # runs up to 4 vectors per launch on the batch-1 16-row kernels.
 @pytest.mark.parametrize("engine", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("case", MM_ENGINE_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
@@ -209,22 +211,30 @@ def _engine_matmul(engine, kind, w, X, in_dim, out_dim):
         dev.set_mm_engine(0)
 
 
+# Decimal exponents of each activation row's magnitude; None = an all-zero
+# row.  Up to 4 rows the one-pass kernel converts through LDS (kq_mmv.hip's
+# staged build), 9 rows in registers.
+ROW_SCALES = [[-30, -12, -3, 0, 0, 3, 12, 30, None], [-30, None, 30, 3], [30, -30]]
+
+
 @pytest.mark.parametrize("engine", [0, 4, 5])
+@pytest.mark.parametrize("exps", ROW_SCALES, ids=lambda e: f"B{len(e)}")
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K])
-def test_mfma_matmul_row_scales(kind, engine):
+def test_mfma_matmul_row_scales(kind, exps, engine):
     """Activation rows spanning 1e-30..1e30 in magnitude (each row is split
-    with its own power-of-two scale) and an all-zero row."""
-    gen = synth.rng(77 + kind)
-    batch, out_dim, in_dim = 9, 192, 1024
+    with its own power-of-two scale) and all-zero rows."""
+    gen = synth.rng(77 + kind + len(exps))
+    batch, out_dim, in_dim = len(exps), 192, 1024
     w = synth.weight_np(kind, out_dim, in_dim, gen)
     X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
-    X *= (10.0 ** np.array([-30, -12, -3, 0, 0, 3, 12, 30, 0]))[:, None].astype(np.float32)
-    X[8] = 0.0
+    X *= (10.0 ** np.array([0 if e is None else e for e in exps]))[:, None].astype(np.float32)
+    zero = [i for i, e in enumerate(exps) if e is None]
+    X[zero] = 0.0
     Y = _engine_matmul(engine, kind, w, X, in_dim, out_dim)
     want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
     assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
                         what=f"{aa.KIND_NAMES[kind]} scaled rows")
-    assert np.all(Y[8] == 0.0)
+    assert np.all(Y[zero] == 0.0)
 
 
 @pytest.mark.parametrize("engine", [0, 4, 5])
