@@ -274,13 +274,11 @@ struct MvWorkspace {
 // where the kind has one.
 // The pick for Q4_K and Q6_K (measured on MI355X at 4096x4096 and
 // 14336x4096, `small_batch` of bench.py):
-//   up to 4 vectors: the batch-1 kernel on 4 vectors (Q6_K; Q4_K where its
-//     batch-1 plan is 16-row workgroups), else one-pass above 2 vectors and
-//     the VALU kernel at 2;
+//   up to 4 vectors: the batch-1 kernel on 4 vectors where its batch-1
+//     plan is 16-row workgroups (and Q6_K at 2 vectors), else one pass;
 //   5-16 vectors: one pass;
-//   above 16: one pass for Q6_K; Q4_K on the 64-vector kernel in one launch,
-//     or the 16-vector one on matrices of at least MM16_MIN_UNITS (64-row
-//     tile, super-block column) pairs.
+//   above 16: one pass for Q6_K; Q4_K on the 64-vector kernel in one launch.
+// The 16-vector kernel stays an engine of its own (3).
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;

@@ -269,6 +269,7 @@ def kquant_table(torch, aa, synth, seed, stream):
             P[c * pb:(c + 1) * pb].copy_(P[:pb])
         x = torch.randn(inp, device="cuda", generator=g)
         y = torch.empty(out, device="cuda")
+        torch.cuda.synchronize()  # weights and x were written on the default stream
         with torch.cuda.stream(stream):
             sp = stream.cuda_stream
             dev.matvec_packed(kind, P.data_ptr(), inp, out, x.data_ptr(), y.data_ptr(), sp)
@@ -321,6 +322,7 @@ def small_batch_table(torch, aa, synth, seed, stream):
             for B in (2, 4, 8, 16, 32, 64):
                 X = torch.randn(B, inp, device="cuda", generator=g)
                 Y = torch.empty(B, out, device="cuda")
+                torch.cuda.synchronize()  # weights and X were written on the default stream
                 with torch.cuda.stream(stream):
                     dev.matmul_packed(kind, P.data_ptr(), inp, out, B, X.data_ptr(), Y.data_ptr(), stream.cuda_stream)
                     stream.synchronize()
@@ -357,16 +359,12 @@ def small_batch_kernel(aa, kind, inp, out, B):
     aspidagpu.hip) for Q4_K and Q6_K: up to 4 vectors the batch-1 kernel on
     4 vectors where the batch-1 plan is 16-row workgroups (and Q6_K at 2),
     else the one-pass kernel; the one-pass kernel up to 16 vectors and for
-    Q6_K above; Q4_K above 16 on the
-    16-vector MFMA kernel for matrices of >= 2048 64-row-by-256-column blocks,
-    else the 64-vector one."""
+    Q6_K above; Q4_K above 16 on the 64-vector MFMA kernel."""
     if B <= 4:
         b16 = aa.DeviceOps().matvec_plan(kind, inp, out)[5]
         return "kq_mv_mfma16n" if b16 or (kind == aa.Q6_K and B <= 2) else "kq_mmv"
     if B <= 16 or kind == aa.Q6_K:
         return "kq_mmv"
-    if (-(-out // 64)) * (inp // 256) >= 2048:
-        return "kq_mm16_q4k"
     return "kq_mm_mfma"
 
 
@@ -424,6 +422,7 @@ def moe_table(torch, aa, synth, seed, stream, tokens=(1, 8, 32), tag="MoE"):
                                        L["shd"].data_ptr(), L["sgi"].data_ptr(), B["work"].data_ptr(),
                                        B["y"].data_ptr(), sp)
 
+        torch.cuda.synchronize()  # weights and X were written on the default stream
         with torch.cuda.stream(stream):
             run(stream.cuda_stream)
             stream.synchronize()
@@ -675,6 +674,7 @@ def copy_probe(torch, mib):
 def timed_graph(torch, stream, step_fn, steps, warmup):
     """Capture one token, replay `warmup` times, then time `steps` replays
     (wall clock around synchronised replays, and HIP events on the stream)."""
+    torch.cuda.synchronize()  # inputs were written on the default stream
     with torch.cuda.stream(stream):
         step_fn(stream.cuda_stream)
     stream.synchronize()
