@@ -225,19 +225,52 @@ __global__ __launch_bounds__(128 * NWG) void moe_gate_up1(MoeGroupedArgs a, int 
   }
 }
 
+// One (slot, column) unit of a 16-row block whose weights c and activations
+// xv are loaded: the arithmetic of mv_mfma_rows<KIND, MV_ONE, 1> from the
+// image build on (the same results).
+template <int KIND>
+__device__ __forceinline__ float moe1_unit(const MvCol<KIND, 1>& c, float4 xv, MvShared16& sh, int lane) {
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (lane < 17) sh.img[j][lane] = make_uint4(0u, 0u, 0u, 0u);
+  const MvLane L = mv_lane<KIND>(sh.img, lane);
+  float acc[1] = {0.f};
+  mv_column<1, 17>(c, xv, L, sh.img, sh.xsum, (MvHdr<KIND>*)nullptr, lane, acc);
+  float* red = reinterpret_cast<float*>(&sh.img[0][0]);
+  __builtin_amdgcn_wave_barrier();
+  red[lane] = acc[0];
+  __builtin_amdgcn_wave_barrier();
+  const float* rr = red + (lane & 15);
+  return ((rr[0] + rr[16]) + rr[32]) + rr[48];
+}
+
 template <int KIND, int NW>
 __global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
+  constexpr int GB = 64 * Block<KIND>::BYTES;
   __shared__ MvShared16 sh[NW];
   __shared__ float part[MOE1_MAX_UNITS][16];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.x, nsb = a.I / 256, units = (a.top_k + 1) * nsb;
-  for (int u = w; u < units; u += NW) {
-    const int k = u / nsb, c = u % nsb;
-    const uint8_t* M = k < a.top_k ? a.down + (size_t)moe_expert(a, k) * a.d_stride : a.sh_down;
-    const float r = mv_mfma_rows<KIND, MV_ONE, 1>(M, nsb, b >> 2, c, 1, a.h + (size_t)k * a.I, sh[w].img, sh[w].xsum,
-                                                  (MvHdr<KIND>*)nullptr, lane, b & 3);
-    if (lane < 16) part[u][lane] = r;
+  // Units u and u + NW of a wave: both units' weights and activations are
+  // requested before either is multiplied, so their loads overlap.
+  for (int u = w; u < units; u += 2 * NW) {
+    const int v = u + NW < units ? u + NW : u;
+    const int k0 = u / nsb, c0 = u % nsb, k1 = v / nsb, c1 = v % nsb;
+    const uint8_t* M0 = k0 < a.top_k ? a.down + (size_t)moe_expert(a, k0) * a.d_stride : a.sh_down;
+    const uint8_t* M1 = k1 < a.top_k ? a.down + (size_t)moe_expert(a, k1) * a.d_stride : a.sh_down;
+    MvCol<KIND, 1> w0, w1;
+    const float4 x0 = ld_f4(a.h + (size_t)k0 * a.I + (size_t)c0 * 256 + 4 * lane);
+    w0.load(M0 + ((size_t)(b >> 2) * nsb + c0) * GB, lane, b & 3);
+    const float4 x1 = ld_f4(a.h + (size_t)k1 * a.I + (size_t)c1 * 256 + 4 * lane);
+    w1.load(M1 + ((size_t)(b >> 2) * nsb + c1) * GB, lane, b & 3);
+    const float r0 = moe1_unit<KIND>(w0, x0, sh[w], lane);
+    if (lane < 16) part[u][lane] = r0;
+    if (v != u) {
+      const float r1 = moe1_unit<KIND>(w1, x1, sh[w], lane);
+      if (lane < 16) part[v][lane] = r1;
+    }
   }
   __syncthreads();
   if (threadIdx.x < 16) {
