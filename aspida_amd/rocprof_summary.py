@@ -13,12 +13,14 @@ averaged per kernel symbol and grid.  Output is Markdown.
 REGEX into N consecutive parts (labelled #1..#N, in dispatch order) -- e.g.
 a table that runs the same kernels at several sizes one after another.
 
---bench-rows small|kquant (with --traffic) prints one line per row of that
+--bench-rows small|kquant|sweep (with --traffic) prints one line per row of that
 bench.py table instead: the run's dispatches are cut into rows at each random-
 number kernel (every row draws its input first), a row's dispatches into its
 1 + R ncopy products (bench.py's eager call and R graph replays of ncopy
 weight copies), and each product's kernels get their median duration and
-calibrated HBM bytes beside the row's algorithmic bytes.
+calibrated HBM bytes beside the row's algorithmic bytes.  With --pmc COUNTER_CSV
+instead of --traffic: each row's median duration and its counters' means per
+dispatch, with the VALU issue rate and MFMA busy share they imply.
 
 With --traffic, the FETCH_SIZE and WRITE_SIZE runs (KiB per dispatch) are
 turned into HBM bytes per launch of each kernel symbol: each counter is scaled
@@ -136,9 +138,15 @@ BENCH_ROWS = {
     "small": [(k, o, i, b) for k in ("Q4_K", "Q6_K") for o, i in ((4096, 4096), (14336, 4096))
               for b in (2, 4, 8, 16, 32, 64)],
     "kquant": [(k, o, i, 1) for k in _KQ for o, i in ((14336, 4096), (4096, 14336))] + [("Q4_K", 4096, 4096, 1)],
+    # bench.py SWEEP_SHAPES per kind
+    "sweep": [(k, o, i, 1) for k in _KQ for o, i in ((2048, 4096), (4096, 4096), (8192, 4096), (14336, 4096),
+                                                      (28672, 4096), (57344, 4096), (57344, 8192))],
 }
 # Graph replays of each row (one untimed, then the timed ones).
-BENCH_REPLAYS = {"small": 4, "kquant": 5}
+BENCH_REPLAYS = {"small": 4, "kquant": 5, "sweep": 5}
+# Issue-rate reference for --bench-rows with --pmc: MI355X's 1024 SIMDs at its
+# 2400 MHz peak engine clock, each issuing at most one VALU instruction a cycle.
+SIMDS, CLOCK_MHZ = 1024, 2400
 _BLOCK = {"Q4_K": 144, "Q6_K": 210, "Q5_K": 176, "Q3_K": 110, "Q2_K": 84}
 
 
@@ -200,6 +208,34 @@ def bench_rows(table, trace_csv, fetch_csv, write_csv, probe_kib):
               f"{alg / us / 1e3:.0f} | {int(hbm)} | {hbm / wbytes:.3f} |")
 
 
+def bench_rows_pmc(table, trace_csv, pmc_csv):
+    """Per row: the median duration of its kernel (trace run) and the mean
+    per dispatch of every counter of the counter run; VALU issue = SQ_INSTS_VALU
+    / (SIMDS x duration x CLOCK_MHZ), MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES /
+    (SIMDS x duration x CLOCK_MHZ)."""
+    with open(pmc_csv) as f:
+        names = sorted({r["Counter_Name"] for r in csv.DictReader(f)})
+    tr = _row_dispatches(trace_csv)
+    pm = {n: _row_dispatches(pmc_csv, n) for n in names}
+    spec = BENCH_ROWS[table]
+    if len(tr) != len(spec) or any(len(v) != len(spec) for v in pm.values()):
+        raise SystemExit(f"rows found: trace {len(tr)}, counters {[len(v) for v in pm.values()]}; expected {len(spec)}")
+    print(f"Per row: median duration (trace run), counters as the mean per dispatch (counter run); VALU issue "
+          f"and MFMA busy against {SIMDS} SIMDs at {CLOCK_MHZ} MHz for the traced duration:")
+    print()
+    print("| row | kernel | µs | GB/s | " + " | ".join(names) + " | VALU issue | MFMA busy |")
+    print("|---|---|---|---|" + "---|" * len(names) + "---|---|")
+    for r, (kind, o, i, b) in enumerate(spec):
+        us = statistics.median(v for _, v in tr[r])
+        mean = {n: statistics.fmean(v for _, v in pm[n][r]) for n in names}
+        nbytes = _BLOCK[kind] * o * (i // 256) + 4 * (i + o)
+        cyc = SIMDS * us * CLOCK_MHZ
+        valu = mean.get("SQ_INSTS_VALU", 0.0) / cyc
+        mfma = mean.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / cyc
+        print(f"| {kind} {o}x{i} | {tr[r][0][0]} | {us:.2f} | {nbytes / us / 1e3:.0f} | " +
+              " | ".join(f"{mean[n]:.0f}" for n in names) + f" | {valu:.2f} | {mfma:.2f} |")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("trace")
@@ -212,9 +248,12 @@ def main():
     ap.add_argument("--bench-rows", choices=sorted(BENCH_ROWS))
     args = ap.parse_args()
     SEGMENTS.extend((rx, int(n)) for rx, n in args.segment)
+    if args.bench_rows and args.pmc and not args.traffic:
+        bench_rows_pmc(args.bench_rows, args.trace, args.pmc[0])
+        return
     if args.bench_rows:
         if not args.traffic:
-            raise SystemExit("--bench-rows needs --traffic")
+            raise SystemExit("--bench-rows needs --traffic or --pmc")
         bench_rows(args.bench_rows, args.trace, args.traffic[0], args.traffic[1], args.probe_kib)
         return
     if args.traffic:

@@ -58,6 +58,42 @@ def layer_plan(m=MODEL_8B):
             ("down", Q6_K, h, f, "act")]
 
 
+# Rows of the batch-1 size sweep (out, in): 2 to 264 MB of Q4_K.
+SWEEP_SHAPES = ((2048, 4096), (4096, 4096), (8192, 4096), (14336, 4096), (28672, 4096), (57344, 4096),
+                (57344, 8192))
+
+
+def size_sweep_table(torch, aa, synth, seed, stream):
+    """Batch-1 matvec time against size per K-quant (SWEEP_SHAPES, cold HBM as
+    kquant_table), and per kind the least-squares line t = t0 + bytes / R over
+    the rows: t0 is the fixed cost of a launch (start-up, first loads, last
+    column's arithmetic), R the rate at which the launch streams once running.
+    A launch of b bytes reaches b / (t0 + b / R); "bytes_for_70pct" is the
+    smallest size at which that is 70% of the HBM peak (null when R itself is
+    below 70%)."""
+    kinds = (aa.Q2_K, aa.Q3_K, aa.Q4_K, aa.Q5_K, aa.Q6_K)
+    rows = kquant_table(torch, aa, synth, seed, stream,
+                        shapes=[(k, o, i) for k in kinds for (o, i) in SWEEP_SHAPES])
+    out = {"rows": rows, "fit": {}}
+    for k in kinds:
+        name = aa.KIND_NAMES[k]
+        pts = [(aa.weight_bytes(k, i, o) + 4 * (i + o), rows[f"{name} {o}x{i}"]["us"] * 1e-6) for o, i in SWEEP_SHAPES]
+        n = len(pts)
+        mb, mt = sum(b for b, _ in pts) / n, sum(t for _, t in pts) / n
+        slope = sum((b - mb) * (t - mt) for b, t in pts) / sum((b - mb) ** 2 for b, _ in pts)
+        t0 = mt - slope * mb
+        rate = 1.0 / slope / 1e9
+        worst = max(abs(t - (t0 + slope * b)) for b, t in pts)
+        p70 = 0.7 * HBM_PEAK_GBS * 1e9
+        need = p70 * t0 / (1.0 - p70 * slope) if p70 * slope < 1.0 else None
+        out["fit"][name] = {"t0_us": round(t0 * 1e6, 2), "stream_GBps": round(rate, 1),
+                            "max_residual_us": round(worst * 1e6, 2),
+                            "bytes_for_70pct": int(need) if need else None}
+        print(f"# fit {name}: t0 {t0 * 1e6:.2f} us, streaming {rate:.0f} GB/s, max residual {worst * 1e6:.2f} us",
+              file=sys.stderr, flush=True)
+    return out
+
+
 # Launches of one layer: q|k and v share their input and run as one launch.
 LAYER_LAUNCHES = [("qk", "v"), ("o",), ("gate_up",), ("down",)]
 # Token counts of the MoE prefill rows (the grouped-GEMM path from 96 tokens).
@@ -73,7 +109,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--only", choices=["small", "moe", "kquant", "decode70", "chain", "prefill"],
+    ap.add_argument("--only", choices=["small", "moe", "kquant", "sweep", "decode70", "chain", "prefill"],
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
@@ -247,16 +283,17 @@ def measured_traffic(kernel):
     return None if k is None else k["traffic_bytes_per_launch"]
 
 
-def kquant_table(torch, aa, synth, seed, stream):
+def kquant_table(torch, aa, synth, seed, stream, shapes=None):
     """Batch-1 matvec per K-quant at the Llama-3-8B FFN shapes (and the 4096^2
     Q4_K q_proj), packed layout, rotating launches over >=1 GiB of distinct
     weight copies so every launch reads cold HBM; one graph of all copies,
-    replayed."""
+    replayed.  `shapes`: (kind, out, in) rows instead of those."""
     dev = aa.DeviceOps()
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 1)
-    shapes = [(k, o, i) for k in (aa.Q2_K, aa.Q3_K, aa.Q4_K, aa.Q5_K, aa.Q6_K)
-              for (o, i) in ((14336, 4096), (4096, 14336))] + [(aa.Q4_K, 4096, 4096)]
+    if shapes is None:
+        shapes = [(k, o, i) for k in (aa.Q2_K, aa.Q3_K, aa.Q4_K, aa.Q5_K, aa.Q6_K)
+                  for (o, i) in ((14336, 4096), (4096, 14336))] + [(aa.Q4_K, 4096, 4096)]
     table = {}
     for kind, out, inp in shapes:
         pb = dev.packed_bytes(kind, inp, out)
@@ -748,7 +785,8 @@ def main():
             print(json.dumps({"moe_prefill": moe_table(torch, aa, synth, args.seed, stream, PREFILL_TOKENS,
                                                         "MoE prefill")}), flush=True)
             return
-        fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table}[args.only]
+        fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table,
+              "sweep": size_sweep_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
         return
     dec = Decoder(torch, aa, synth, args.seed, args.mv_engine)
