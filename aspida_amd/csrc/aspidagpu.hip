@@ -277,7 +277,8 @@ struct MvWorkspace {
 //   up to 4 vectors: the batch-1 kernel on 4 vectors where its batch-1
 //     plan is 16-row workgroups (and Q6_K at 2 vectors), else one pass;
 //   5-16 vectors: one pass;
-//   above 16: one pass for Q6_K; Q4_K on the 64-vector kernel in one launch.
+//   above 16: one pass for Q6_K (launches of 32 vectors on 64-row tiles);
+//     Q4_K on the 64-vector kernel in one launch.
 // The 16-vector kernel stays an engine of its own (3).
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
@@ -311,7 +312,7 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
       if (kq::mfma_plan(kind, in_dim, out_dim).blk16 || (kind == kq::Q6_K && batch <= 2)) return {4, 4};
       return {3, 64};
     }
-    if (batch <= 16 || kind == kq::Q6_K) return {3, 64};
+    if (batch <= 16 || kind == kq::Q6_K) return {3, kq::mmv_step(kind, in_dim, out_dim)};
   }
   if (mm16) return {1, 16};
   if (mm64) return {2, kind == kq::Q6_K ? 32 : 64};

@@ -101,6 +101,9 @@ hipError_t launch_matvec_mfma_nv(int kind, const void* P, int in_dim, int out_di
 // cores with the batch-1 work split (kq_mmv.hip): every weight byte read once,
 // no workspace, no pre-pass.  x must be 16-byte aligned.
 bool mmv_kind(int kind);
+// Vectors per launch for larger batches: 32 for Q6_K on 64-row tiles (whose
+// four-group launch would run on 4 waves), else 64.
+int mmv_step(int kind, int in_dim, int out_dim);
 hipError_t launch_matmul_mmv(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
                              hipStream_t s);
 bool mm16_kind(int kind);
