@@ -20,7 +20,7 @@ number kernel (every row draws its input first), a row's dispatches into its
 weight copies), and each product's kernels get their median duration and
 calibrated HBM bytes beside the row's algorithmic bytes.  With --pmc COUNTER_CSV
 instead of --traffic: each row's median duration and its counters' means per
-dispatch, with the VALU issue rate and MFMA busy share they imply.
+dispatch, with the VALU and MFMA busy shares they imply.
 
 With --traffic, the FETCH_SIZE and WRITE_SIZE runs (KiB per dispatch) are
 turned into HBM bytes per launch of each kernel symbol: each counter is scaled
@@ -144,9 +144,11 @@ BENCH_ROWS = {
 }
 # Graph replays of each row (one untimed, then the timed ones).
 BENCH_REPLAYS = {"small": 4, "kquant": 5, "sweep": 5}
-# Issue-rate reference for --bench-rows with --pmc: MI355X's 1024 SIMDs at its
-# 2400 MHz peak engine clock, each issuing at most one VALU instruction a cycle.
-SIMDS, CLOCK_MHZ = 1024, 2400
+# Busy-share reference for --bench-rows with --pmc: MI355X's 1024 SIMDs at its
+# 2400 MHz peak engine clock.  A SIMD's vector ALU is 16 lanes wide, so a
+# wave64 VALU instruction occupies it for 4 cycles (VALU_CYCLES); matrix-core
+# instructions are counted in SQ_INSTS_VALU too and are taken out of it.
+SIMDS, CLOCK_MHZ, VALU_CYCLES = 1024, 2400, 4
 _BLOCK = {"Q4_K": 144, "Q6_K": 210, "Q5_K": 176, "Q3_K": 110, "Q2_K": 84}
 
 
@@ -210,9 +212,10 @@ def bench_rows(table, trace_csv, fetch_csv, write_csv, probe_kib):
 
 def bench_rows_pmc(table, trace_csv, pmc_csv):
     """Per row: the median duration of its kernel (trace run) and the mean
-    per dispatch of every counter of the counter run; VALU issue = SQ_INSTS_VALU
-    / (SIMDS x duration x CLOCK_MHZ), MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES /
-    (SIMDS x duration x CLOCK_MHZ)."""
+    per dispatch of every counter of the counter run; VALU busy =
+    (SQ_INSTS_VALU - SQ_INSTS_MFMA) x VALU_CYCLES / (SIMDS x duration x
+    CLOCK_MHZ), MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDS x duration x
+    CLOCK_MHZ)."""
     with open(pmc_csv) as f:
         names = sorted({r["Counter_Name"] for r in csv.DictReader(f)})
     tr = _row_dispatches(trace_csv)
@@ -220,17 +223,18 @@ def bench_rows_pmc(table, trace_csv, pmc_csv):
     spec = BENCH_ROWS[table]
     if len(tr) != len(spec) or any(len(v) != len(spec) for v in pm.values()):
         raise SystemExit(f"rows found: trace {len(tr)}, counters {[len(v) for v in pm.values()]}; expected {len(spec)}")
-    print(f"Per row: median duration (trace run), counters as the mean per dispatch (counter run); VALU issue "
-          f"and MFMA busy against {SIMDS} SIMDs at {CLOCK_MHZ} MHz for the traced duration:")
+    print(f"Per row: median duration (trace run), counters as the mean per dispatch (counter run); VALU busy "
+          f"({VALU_CYCLES} cycles per non-MFMA VALU instruction) and MFMA busy against {SIMDS} SIMDs at {CLOCK_MHZ} MHz "
+          f"for the traced duration:")
     print()
-    print("| row | kernel | µs | GB/s | " + " | ".join(names) + " | VALU issue | MFMA busy |")
+    print("| row | kernel | µs | GB/s | " + " | ".join(names) + " | VALU busy | MFMA busy |")
     print("|---|---|---|---|" + "---|" * len(names) + "---|---|")
     for r, (kind, o, i, b) in enumerate(spec):
         us = statistics.median(v for _, v in tr[r])
         mean = {n: statistics.fmean(v for _, v in pm[n][r]) for n in names}
         nbytes = _BLOCK[kind] * o * (i // 256) + 4 * (i + o)
         cyc = SIMDS * us * CLOCK_MHZ
-        valu = mean.get("SQ_INSTS_VALU", 0.0) / cyc
+        valu = (mean.get("SQ_INSTS_VALU", 0.0) - mean.get("SQ_INSTS_MFMA", 0.0)) * VALU_CYCLES / cyc
         mfma = mean.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / cyc
         print(f"| {kind} {o}x{i} | {tr[r][0][0]} | {us:.2f} | {nbytes / us / 1e3:.0f} | " +
               " | ".join(f"{mean[n]:.0f}" for n in names) + f" | {valu:.2f} | {mfma:.2f} |")
