@@ -176,14 +176,16 @@ def test_mfma_matmul_matches_oracle(kind, case):
 # one column per wave and long column runs, tiles split over workgroups.
 MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304), (40, 4096, 4096),
                    (9, 16448, 2048), (3, 256, 14336), (20, 12352, 512), (64, 12352, 256), (63, 300, 1024),
-                   (2, 13000, 256), (4, 12352, 512)]
+                   (2, 13000, 256), (4, 12352, 512), (48, 12352, 512), (61, 13000, 256)]
 
 
 # Engine 4 is the one-pass kernel (kq_mmv.hip): 64-row tiles from 12352 rows
 # (193 tiles), 16-row blocks below; up to 64 vectors in one launch, up to 4
 # converted through LDS.  Engine 5
-# runs up to 4 vectors per launch on the batch-1 16-row kernels.
-@pytest.mark.parametrize("engine", [1, 2, 3, 4, 5])
+# runs up to 4 vectors per launch on the batch-1 16-row kernels.  Engine 0 is
+# the library's pick (Q6_K on 64-row tiles above 32 vectors: launches of 32
+# on the one-pass kernel).
+@pytest.mark.parametrize("engine", [0, 1, 2, 3, 4, 5])
 @pytest.mark.parametrize("case", MM_ENGINE_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
 def test_mm_engines_match_oracle(kind, case, engine):
