@@ -250,9 +250,12 @@ __global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
   constexpr int GB = 64 * Block<KIND>::BYTES;
   __shared__ MvShared16 sh[NW];
   __shared__ float part[MOE1_MAX_UNITS][16];
+  __shared__ float wk[MOE_MAX_TOPK + 1];  // the combine's slot weights, top_w[k] and g last
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.x, nsb = a.I / 256, units = (a.top_k + 1) * nsb;
+  // Requested now, with the first loads, rather than one after another in the combine.
+  if ((int)threadIdx.x <= a.top_k) wk[threadIdx.x] = (int)threadIdx.x < a.top_k ? a.top_w[threadIdx.x] : a.gsh[0];
   // Units u and u + NW of a wave: both units' weights and activations are
   // requested before either is multiplied, so their loads overlap.
   for (int u = w; u < units; u += 2 * NW) {
@@ -279,7 +282,7 @@ __global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
     for (int k = 0; k <= a.top_k; ++k) {
       float s = 0.f;
       for (int c = 0; c < nsb; ++c) s += part[k * nsb + c][t];
-      acc = acc + (k < a.top_k ? a.top_w[k] : a.gsh[0]) * s;
+      acc = acc + wk[k] * s;
     }
     a.y[16 * b + t] = acc;
   }
