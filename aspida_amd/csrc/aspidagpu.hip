@@ -913,6 +913,24 @@ extern "C" int aspida_moe_route_dev(const float* router_w, int n_exp, int dim, i
                "aspida_moe_route_dev");
 }
 
+namespace kq {
+// The model chain's router step with the post-attention norm in the same
+// launch (launch_moe_route_norm): 0, -ENOTSUP when the shape does not take
+// it, or the error.
+int route_norm_dev(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
+                   const float* g, float* nx, float* logits, int* top_idx, float* top_w, void* stream) {
+  if (!moe_route_norm_takes(n_exp, dim, T, top_k)) return -ENOTSUP;
+  if (!router_w || !H || !g || !nx || !logits || !top_idx || !top_w || ((uintptr_t)router_w & 15) ||
+      ((uintptr_t)H & 15) || ((uintptr_t)nx & 15) || ((uintptr_t)g & 15) || (r && ((uintptr_t)r & 15)))
+    return -EINVAL;
+  MvWorkspace* ws = stream_workspace(stream, 256, moe_route_groups(T) * 64, 1);
+  if (!ws) return t_last_error ? t_last_error : -1;
+  return check(launch_moe_route_norm(router_w, n_exp, dim, T, top_k, H, r, g, nx, logits, top_idx, top_w, ws->count.p,
+                                     (hipStream_t)stream),
+               "chain router with norm");
+}
+}  // namespace kq
+
 extern "C" long aspida_moe_work_floats(int T, int dim, int top_k, int intermed) {
   kq::MoeWeights w;
   w.dim = dim;

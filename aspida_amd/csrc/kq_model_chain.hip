@@ -40,6 +40,9 @@
 
 namespace kq {
 void abi_report(int code, const char* what);  // aspidagpu.hip: the calling thread's aspida_gpu_last_error
+// aspidagpu.hip: the router with the norm before it in one launch (0, -ENOTSUP or an error).
+int route_norm_dev(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
+                   const float* g, float* nx, float* logits, int* top_idx, float* top_w, void* stream);
 }  // namespace kq
 
 namespace {
@@ -285,10 +288,19 @@ int add_norm(Chain& c, int B, const float* r, const float* w) {
   return hip(hipGetLastError(), "chain norm");
 }
 
+// The post-attention norm and the router: one launch where the router can
+// form its own input (every workgroup normalises its tokens' rows; the last
+// one writes H + r and the norm's output back), else the norm launch and
+// then the router.
+int norm_route(Chain& c, const Layer& L, int B, const float* pend) {
+  const int rc = kq::route_norm_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.H, pend, L.post_norm, c.nx, c.rl, c.idx,
+                                    c.tw, c.st);
+  if (rc != -ENOTSUP) return rc ? fail(rc, "chain router with norm") : 0;
+  if (int rc2 = add_norm(c, B, pend, L.post_norm)) return rc2;
+  return ep(aspida_moe_route_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.nx, c.rl, c.idx, c.tw, c.st), "chain router");
+}
+
 int moe_apply(Chain& c, const Layer& L, int B) {
-  if (int rc = ep(aspida_moe_route_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.nx, c.rl, c.idx, c.tw, c.st),
-                  "chain router"))
-    return rc;
   if (L.grouped)
     return ep(aspida_moe_experts_packed_dev(c.nx, B, c.dim, L.top_k, L.intermed, L.n_exp, c.idx, c.tw, L.g, L.u, L.gk,
                                             L.dn, L.dk, L.sg, L.su, L.sd, L.sgi, c.work, c.y, c.st),
@@ -315,7 +327,7 @@ int record(Chain& c, int B, int n_layers, bool logits) {
       pend = c.ao;
     }
     if (L.has_moe) {
-      if (int rc = add_norm(c, B, pend, L.post_norm)) return rc;
+      if (int rc = norm_route(c, L, B, pend)) return rc;
       if (int rc = moe_apply(c, L, B)) return rc;
       pend = c.y;
     }

@@ -395,10 +395,62 @@ __device__ __forceinline__ void route_select_wg(RouteLds& L, const float* logits
   }
 }
 
+// The router's input formed in the same launch (NORM): x = RMSNorm(H + r)
+// with weights g, as a model's post-attention norm (LLM_RMSNorm.Forward,
+// src/llm/llm_rmsnorm.adb:10-41, Epsilon 1e-6 of llm_rmsnorm.ads:19): every
+// workgroup forms its tokens' x in LDS -- the sum of squares in the order of
+// a one-workgroup norm of 256 threads, so x is the same -- and the last
+// workgroup of a token group to arrive writes H + r back to H and x to nx
+// (no workgroup of the launch reads those rows after it).
+constexpr int ROUTE_NORM_MAX_DIM = 4096;
+struct RouteNorm {
+  const float* r;  // residual to add to H, or null
+  const float* g;  // norm weights [dim]
+  float* H;        // [T][dim], read (and written back when r is given)
+  float* nx;       // [T][dim] the normalised input
+};
+
+__device__ __forceinline__ void route_norm_rows(const RouteNorm& nm, float (&xs)[ROUTE_TT][ROUTE_NORM_MAX_DIM],
+                                                float* part, int t0, int nt, int dim) {
+  const int n4 = dim / 4;
+  for (int tt = 0; tt < nt; ++tt) {
+    const float4* h = reinterpret_cast<const float4*>(nm.H + (size_t)(t0 + tt) * dim);
+    const float4* rr = nm.r ? reinterpret_cast<const float4*>(nm.r + (size_t)(t0 + tt) * dim) : nullptr;
+    float4* xs4 = reinterpret_cast<float4*>(xs[tt]);
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n4; i += 256) {
+      float4 v = h[i];
+      if (rr) {
+        const float4 a = rr[i];
+        v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+      }
+      xs4[i] = v;
+      s += v.x * v.x;
+      s += v.y * v.y;
+      s += v.z * v.z;
+      s += v.w * v.w;
+    }
+    s = wave_total(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) tot += part[k];
+    const float rms = sqrtf(tot / (float)dim + 1e-6f);
+    const float4* g4 = reinterpret_cast<const float4*>(nm.g);
+    for (int i = threadIdx.x; i < n4; i += 256) {
+      const float4 v = xs4[i], g = g4[i];
+      xs4[i] = make_float4((v.x / rms) * g.x, (v.y / rms) * g.y, (v.z / rms) * g.z, (v.w / rms) * g.w);
+    }
+    __syncthreads();
+  }
+}
+
+template <bool NORM>
 __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, int n_exp, int dim, int T,
                                                  const float* __restrict__ x, int top_k, float* __restrict__ logits,
                                                  int* __restrict__ top_idx, float* __restrict__ top_w,
-                                                 unsigned* __restrict__ count) {
+                                                 unsigned* __restrict__ count, RouteNorm nm) {
   __shared__ int last;
   __shared__ RouteLds sel;
   const int lane = threadIdx.x & 63;
@@ -407,6 +459,9 @@ __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, in
   const int t0 = blockIdx.y * ROUTE_TT;
   const int nt = T - t0 < ROUTE_TT ? T - t0 : ROUTE_TT;
   const int n4 = dim / 4;
+  __shared__ float normpart[4];
+  __shared__ float xs[NORM ? ROUTE_TT : 1][NORM ? ROUTE_NORM_MAX_DIM : 4];
+  if constexpr (NORM) route_norm_rows(nm, xs, normpart, t0, nt, dim);
   if (e < n_exp) {
     // Rows are read in blocks of RB float4 per lane, all loads of a block in
     // flight together: indices are clamped (and the products of the padding
@@ -425,7 +480,7 @@ __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, in
       }
 #pragma unroll
       for (int tt = 0; tt < ROUTE_TT; ++tt) {
-        const float4* xt = x4 + (size_t)(tt < nt ? tt : 0) * n4;
+        const float4* xt = NORM ? reinterpret_cast<const float4*>(xs[tt < nt ? tt : 0]) : x4 + (size_t)(tt < nt ? tt : 0) * n4;
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
           const int i = b + 64 * r + lane;
@@ -457,6 +512,22 @@ __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, in
   }
   __syncthreads();
   if (!last) return;
+  if constexpr (NORM) {
+    // This token group's rows: H + r back to H, x to nx.
+    for (int tt = 0; tt < nt; ++tt) {
+      float4* h = reinterpret_cast<float4*>(nm.H + (size_t)(t0 + tt) * dim);
+      const float4* rr = nm.r ? reinterpret_cast<const float4*>(nm.r + (size_t)(t0 + tt) * dim) : nullptr;
+      float4* y = reinterpret_cast<float4*>(nm.nx + (size_t)(t0 + tt) * dim);
+      const float4* xs4 = reinterpret_cast<const float4*>(xs[tt]);
+      for (int i = threadIdx.x; i < n4; i += 256) {
+        if (rr) {
+          const float4 v = h[i], a = rr[i];
+          h[i] = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+        }
+        y[i] = xs4[i];
+      }
+    }
+  }
   if (n_exp <= 256) {
     // G waves per token: all four for one token, two each for two, one each for more.
 #define KQ_SEL(PER)                                                                                 \
@@ -573,8 +644,23 @@ hipError_t launch_moe_route(const float* router_w, int n_exp, int dim, int T, in
     return hipGetLastError();
   }
   const dim3 grid((n_exp + 3) / 4, (T + ROUTE_TT - 1) / ROUTE_TT);
-  hipLaunchKernelGGL(moe_route, grid, dim3(256), 0, s, router_w, n_exp, dim, T, x, top_k, logits, top_idx, top_w,
-                     count);
+  hipLaunchKernelGGL(moe_route<false>, grid, dim3(256), 0, s, router_w, n_exp, dim, T, x, top_k, logits, top_idx,
+                     top_w, count, RouteNorm{});
+  return hipGetLastError();
+}
+
+bool moe_route_norm_takes(int n_exp, int dim, int T, int top_k) {
+  return n_exp > 0 && n_exp <= ROUTE_MAX_EXP && top_k > 0 && top_k <= MOE_MAX_TOPK && top_k <= n_exp && top_k <= 64 &&
+         dim > 0 && dim % 4 == 0 && dim <= ROUTE_NORM_MAX_DIM && T > 0 && !route_tokens_takes(T, dim);
+}
+
+hipError_t launch_moe_route_norm(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
+                                 const float* g, float* nx, float* logits, int* top_idx, float* top_w, unsigned* count,
+                                 hipStream_t s) {
+  if (!moe_route_norm_takes(n_exp, dim, T, top_k) || !H || !g || !nx || !logits || !count) return hipErrorInvalidValue;
+  const dim3 grid((n_exp + 3) / 4, (T + ROUTE_TT - 1) / ROUTE_TT);
+  hipLaunchKernelGGL(moe_route<true>, grid, dim3(256), 0, s, router_w, n_exp, dim, T, (const float*)nullptr, top_k,
+                     logits, top_idx, top_w, count, RouteNorm{r, g, H, nx});
   return hipGetLastError();
 }
 
