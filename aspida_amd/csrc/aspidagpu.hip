@@ -918,16 +918,29 @@ namespace kq {
 // launch (launch_moe_route_norm): 0, -ENOTSUP when the shape does not take
 // it, or the error.
 int route_norm_dev(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
-                   const float* g, float* nx, float* logits, int* top_idx, float* top_w, void* stream) {
+                   const float* r2, const float* g, float* nx, float* logits, int* top_idx, float* top_w,
+                   void* stream) {
   if (!moe_route_norm_takes(n_exp, dim, T, top_k)) return -ENOTSUP;
   if (!router_w || !H || !g || !nx || !logits || !top_idx || !top_w || ((uintptr_t)router_w & 15) ||
-      ((uintptr_t)H & 15) || ((uintptr_t)nx & 15) || ((uintptr_t)g & 15) || (r && ((uintptr_t)r & 15)))
+      ((uintptr_t)H & 15) || ((uintptr_t)nx & 15) || ((uintptr_t)g & 15) || (r && ((uintptr_t)r & 15)) ||
+      (r2 && ((uintptr_t)r2 & 15)))
     return -EINVAL;
   MvWorkspace* ws = stream_workspace(stream, 256, moe_route_groups(T) * 64, 1);
   if (!ws) return t_last_error ? t_last_error : -1;
-  return check(launch_moe_route_norm(router_w, n_exp, dim, T, top_k, H, r, g, nx, logits, top_idx, top_w, ws->count.p,
-                                     (hipStream_t)stream),
+  return check(launch_moe_route_norm(router_w, n_exp, dim, T, top_k, H, r, r2, g, nx, logits, top_idx, top_w,
+                                     ws->count.p, (hipStream_t)stream),
                "chain router with norm");
+}
+
+// The model chain's one-lane mixer with the attention norm in the same
+// launch (launch_matvec_norm): 0, -ENOTSUP when the shape does not take it,
+// or the error.
+int matvec_norm_dev(int kind, const void* P, int in_dim, int out_dim, const float* H, const float* r, const float* g,
+                    float* y, void* stream) {
+  if (!matvec_norm_takes(kind, in_dim, out_dim)) return -ENOTSUP;
+  if (!P || !H || !g || !y || ((uintptr_t)H & 15) || ((uintptr_t)g & 15) || (r && ((uintptr_t)r & 15)))
+    return -EINVAL;
+  return check(launch_matvec_norm(kind, P, in_dim, out_dim, H, r, g, y, (hipStream_t)stream), "chain mixer with norm");
 }
 }  // namespace kq
 

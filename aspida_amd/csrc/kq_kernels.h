@@ -127,6 +127,13 @@ hipError_t launch_pack(int kind, const void* src, int in_dim, int out_dim, void*
 // (comparison), 0 restores the default.
 void set_matvec_engine(int engine);
 bool matvec_mfma_takes(int kind);
+// The 16-row matrix-core matvec with its x formed in the launch: x =
+// RMSNorm(H + r) with weights g (r may be null; H is not written).  Q4_K and
+// Q6_K whose batch-1 plan is 16-row workgroups of at least 4 waves, in_dim
+// <= 4096 (matvec_norm_takes).
+bool matvec_norm_takes(int kind, int in_dim, int out_dim);
+hipError_t launch_matvec_norm(int kind, const void* P, int in_dim, int out_dim, const float* H, const float* r,
+                              const float* g, float* y, hipStream_t s);
 hipError_t launch_matvec_mfma(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y, float* part,
                               unsigned* count, hipStream_t s);
 // The fused pair on MFMA when both kinds are MFMA kinds (launch_matvec2_packed

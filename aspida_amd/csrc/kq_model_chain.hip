@@ -40,9 +40,14 @@
 
 namespace kq {
 void abi_report(int code, const char* what);  // aspidagpu.hip: the calling thread's aspida_gpu_last_error
-// aspidagpu.hip: the router with the norm before it in one launch (0, -ENOTSUP or an error).
+// aspidagpu.hip: the router with the norm before it in one launch, and the
+// one-lane mixer with the norm before it (0, -ENOTSUP or an error).
 int route_norm_dev(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
-                   const float* g, float* nx, float* logits, int* top_idx, float* top_w, void* stream);
+                   const float* r2, const float* g, float* nx, float* logits, int* top_idx, float* top_w,
+                   void* stream);
+int matvec_norm_dev(int kind, const void* P, int in_dim, int out_dim, const float* H, const float* r, const float* g,
+                    float* y, void* stream);
+bool moe_route_norm_takes(int n_exp, int dim, int T, int top_k);  // kq_moe.hip
 }  // namespace kq
 
 namespace {
@@ -289,14 +294,16 @@ int add_norm(Chain& c, int B, const float* r, const float* w) {
 }
 
 // The post-attention norm and the router: one launch where the router can
-// form its own input (every workgroup normalises its tokens' rows; the last
-// one writes H + r and the norm's output back), else the norm launch and
-// then the router.
-int norm_route(Chain& c, const Layer& L, int B, const float* pend) {
-  const int rc = kq::route_norm_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.H, pend, L.post_norm, c.nx, c.rl, c.idx,
-                                    c.tw, c.st);
-  if (rc != -ENOTSUP) return rc ? fail(rc, "chain router with norm") : 0;
+// form its own input (every workgroup normalises its tokens' rows of H +
+// pend + pend2; the last one writes the sum and the norm's output back),
+// else norm launches and then the router.
+int norm_route(Chain& c, const Layer& L, int B, const float* pend, const float* pend2) {
+  const int rc = kq::route_norm_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.H, pend, pend2, L.post_norm, c.nx, c.rl,
+                                    c.idx, c.tw, c.st);
+  if (rc != -ENOTSUP) return ep(rc, "chain router with norm");
   if (int rc2 = add_norm(c, B, pend, L.post_norm)) return rc2;
+  if (pend2)
+    if (int rc2 = add_norm(c, B, pend2, L.post_norm)) return rc2;
   return ep(aspida_moe_route_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.nx, c.rl, c.idx, c.tw, c.st), "chain router");
 }
 
@@ -321,13 +328,26 @@ int record(Chain& c, int B, int n_layers, bool logits) {
   const float* pend = nullptr;  // the residual still to be added to H
   for (int l = 0; l < n_layers; ++l) {
     const Layer& L = c.layers[l];
+    if (L.has_mix && B == 1 && L.has_moe && L.mix.kind >= 0 &&
+        kq::moe_route_norm_takes(L.n_exp, c.dim, B, L.top_k)) {
+      // One lane: the attention norm inside the mixer launch (H not written)
+      // and the router adding both residuals, pend then the mixer's output.
+      const int rc = kq::matvec_norm_dev(L.mix.kind, L.mix.d, L.mix.in, L.mix.out, c.H, pend, L.attn_norm, c.ao, c.st);
+      if (rc == 0) {
+        if (int rc2 = norm_route(c, L, B, pend, c.ao)) return rc2;
+        if (int rc2 = moe_apply(c, L, B)) return rc2;
+        pend = c.y;
+        continue;
+      }
+      if (rc != -ENOTSUP) return ep(rc, "chain mixer with norm");
+    }
     if (L.has_mix) {
       if (int rc = add_norm(c, B, pend, L.attn_norm)) return rc;
       if (int rc = mat_apply(c, L.mix, B, c.nx, c.ao)) return rc;
       pend = c.ao;
     }
     if (L.has_moe) {
-      if (int rc = norm_route(c, L, B, pend)) return rc;
+      if (int rc = norm_route(c, L, B, pend, nullptr)) return rc;
       if (int rc = moe_apply(c, L, B)) return rc;
       pend = c.y;
     }

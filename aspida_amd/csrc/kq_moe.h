@@ -116,13 +116,14 @@ hipError_t launch_moe_prefill(const MoeGroupedArgs& a, void* work, hipStream_t s
 hipError_t launch_moe_route(const float* router_w, int n_exp, int dim, int T, int top_k, const float* x,
                             float* logits, int* top_idx, float* top_w, unsigned* count, hipStream_t s);
 int moe_route_groups(int T);
-// The router with its input normalised in the same launch: x = RMSNorm(H + r)
-// with weights g (r may be null); H + r is written back to H and x to nx.
-// Arguments otherwise as launch_moe_route; dim <= 4096 and T below the
-// many-token router's range (moe_route_norm_takes).
+// The router with its input normalised in the same launch: x = RMSNorm(H +
+// r + r2) with weights g (r, r2 may be null; added in that order); the sum
+// is written back to H and x to nx.  Arguments otherwise as
+// launch_moe_route; dim <= 4096 and T below the many-token router's range
+// (moe_route_norm_takes).
 bool moe_route_norm_takes(int n_exp, int dim, int T, int top_k);
 hipError_t launch_moe_route_norm(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
-                                 const float* g, float* nx, float* logits, int* top_idx, float* top_w, unsigned* count,
-                                 hipStream_t s);
+                                 const float* r2, const float* g, float* nx, float* logits, int* top_idx, float* top_w,
+                                 unsigned* count, hipStream_t s);
 
 }  // namespace kq

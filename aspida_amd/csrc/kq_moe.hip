@@ -395,8 +395,8 @@ __device__ __forceinline__ void route_select_wg(RouteLds& L, const float* logits
   }
 }
 
-// The router's input formed in the same launch (NORM): x = RMSNorm(H + r)
-// with weights g, as a model's post-attention norm (LLM_RMSNorm.Forward,
+// The router's input formed in the same launch (NORM): x = RMSNorm(H + r
+// (+ r2)) with weights g, as a model's post-attention norm (LLM_RMSNorm.Forward,
 // src/llm/llm_rmsnorm.adb:10-41, Epsilon 1e-6 of llm_rmsnorm.ads:19): every
 // workgroup forms its tokens' x in LDS -- the sum of squares in the order of
 // a one-workgroup norm of 256 threads, so x is the same -- and the last
@@ -405,6 +405,7 @@ __device__ __forceinline__ void route_select_wg(RouteLds& L, const float* logits
 constexpr int ROUTE_NORM_MAX_DIM = 4096;
 struct RouteNorm {
   const float* r;  // residual to add to H, or null
+  const float* r2; // a second one, added after r, or null
   const float* g;  // norm weights [dim]
   float* H;        // [T][dim], read (and written back when r is given)
   float* nx;       // [T][dim] the normalised input
@@ -416,12 +417,17 @@ __device__ __forceinline__ void route_norm_rows(const RouteNorm& nm, float (&xs)
   for (int tt = 0; tt < nt; ++tt) {
     const float4* h = reinterpret_cast<const float4*>(nm.H + (size_t)(t0 + tt) * dim);
     const float4* rr = nm.r ? reinterpret_cast<const float4*>(nm.r + (size_t)(t0 + tt) * dim) : nullptr;
+    const float4* rr2 = nm.r2 ? reinterpret_cast<const float4*>(nm.r2 + (size_t)(t0 + tt) * dim) : nullptr;
     float4* xs4 = reinterpret_cast<float4*>(xs[tt]);
     float s = 0.f;
     for (int i = threadIdx.x; i < n4; i += 256) {
       float4 v = h[i];
       if (rr) {
         const float4 a = rr[i];
+        v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+      }
+      if (rr2) {
+        const float4 a = rr2[i];
         v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
       }
       xs4[i] = v;
@@ -517,12 +523,21 @@ __global__ __launch_bounds__(256) void moe_route(const float* __restrict__ W, in
     for (int tt = 0; tt < nt; ++tt) {
       float4* h = reinterpret_cast<float4*>(nm.H + (size_t)(t0 + tt) * dim);
       const float4* rr = nm.r ? reinterpret_cast<const float4*>(nm.r + (size_t)(t0 + tt) * dim) : nullptr;
+      const float4* rr2 = nm.r2 ? reinterpret_cast<const float4*>(nm.r2 + (size_t)(t0 + tt) * dim) : nullptr;
       float4* y = reinterpret_cast<float4*>(nm.nx + (size_t)(t0 + tt) * dim);
       const float4* xs4 = reinterpret_cast<const float4*>(xs[tt]);
       for (int i = threadIdx.x; i < n4; i += 256) {
-        if (rr) {
-          const float4 v = h[i], a = rr[i];
-          h[i] = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+        if (rr || rr2) {
+          float4 v = h[i];
+          if (rr) {
+            const float4 a = rr[i];
+            v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+          }
+          if (rr2) {
+            const float4 a = rr2[i];
+            v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+          }
+          h[i] = v;
         }
         y[i] = xs4[i];
       }
@@ -655,12 +670,12 @@ bool moe_route_norm_takes(int n_exp, int dim, int T, int top_k) {
 }
 
 hipError_t launch_moe_route_norm(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
-                                 const float* g, float* nx, float* logits, int* top_idx, float* top_w, unsigned* count,
-                                 hipStream_t s) {
+                                 const float* r2, const float* g, float* nx, float* logits, int* top_idx, float* top_w,
+                                 unsigned* count, hipStream_t s) {
   if (!moe_route_norm_takes(n_exp, dim, T, top_k) || !H || !g || !nx || !logits || !count) return hipErrorInvalidValue;
   const dim3 grid((n_exp + 3) / 4, (T + ROUTE_TT - 1) / ROUTE_TT);
   hipLaunchKernelGGL(moe_route<true>, grid, dim3(256), 0, s, router_w, n_exp, dim, T, (const float*)nullptr, top_k,
-                     logits, top_idx, top_w, count, RouteNorm{r, g, H, nx});
+                     logits, top_idx, top_w, count, RouteNorm{r, r2, g, H, nx});
   return hipGetLastError();
 }
 

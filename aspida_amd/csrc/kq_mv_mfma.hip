@@ -127,6 +127,60 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma16(const uint8_t* __restric
   mv16_epilogue<NW>(r, blk, out_rows, y);
 }
 
+// The same with x formed in the launch: x = RMSNorm(H + r) with weights g
+// (LLM_RMSNorm.Forward, src/llm/llm_rmsnorm.adb:10-41, Epsilon 1e-6 of
+// llm_rmsnorm.ads:19), as a model's attention norm before its first
+// projection.  Every workgroup forms x in LDS -- threads 0-255 sum the
+// squares in the order of a one-workgroup norm of 256 threads, so x is that
+// norm's bit for bit -- and reads its columns from there; H is not written.
+constexpr int MV_NORM_MAX_DIM = 4096;
+template <int KIND, int NW, int PIPE>
+__global__ __launch_bounds__(64 * NW) void kq_mv_mfma16_norm(const uint8_t* __restrict__ P, int nsb, int out_rows,
+                                                            const float* __restrict__ H, const float* __restrict__ r,
+                                                            const float* __restrict__ g, float* __restrict__ y,
+                                                            int spw) {
+  static_assert(NW >= 4, "the norm's sums take 256 threads");
+  __shared__ MvShared16 sh[NW];
+  __shared__ float4 xs4[MV_NORM_MAX_DIM / 4];
+  __shared__ float part[4];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = blockIdx.x, dim = nsb * 256, n4 = dim / 4;
+  const float4* h4 = reinterpret_cast<const float4*>(H);
+  const float4* r4 = reinterpret_cast<const float4*>(r);
+  if (threadIdx.x < 256) {
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n4; i += 256) {
+      float4 v = h4[i];
+      if (r4) {
+        const float4 a = r4[i];
+        v = make_float4(v.x + a.x, v.y + a.y, v.z + a.z, v.w + a.w);
+      }
+      xs4[i] = v;
+      ss += v.x * v.x;
+      ss += v.y * v.y;
+      ss += v.z * v.z;
+      ss += v.w * v.w;
+    }
+    ss = wave_total(ss);
+    if (lane == 0) part[w] = ss;
+  }
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) tot += part[k];
+  const float rms = sqrtf(tot / (float)dim + 1e-6f);
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  for (int i = threadIdx.x; i < n4; i += 64 * NW) {
+    const float4 v = xs4[i], gg = g4[i];
+    xs4[i] = make_float4((v.x / rms) * gg.x, (v.y / rms) * gg.y, (v.z / rms) * gg.z, (v.w / rms) * gg.w);
+  }
+  __syncthreads();
+  const float res = mv_mfma_rows<KIND, PIPE, 1>(P, nsb, blk >> 2, w * spw, spw, reinterpret_cast<const float*>(xs4),
+                                                sh[w].img, sh[w].xsum, (MvHdr<KIND>*)nullptr, lane, blk & 3);
+  mv16_epilogue<NW>(res, blk, out_rows, y);
+}
+
 // Two matrices that multiply the same x: blocks [0, blocks_a) are matrix A's.
 template <int KA, int KB, int NW, int PIPE>
 __global__ __launch_bounds__(64 * NW) void kq_mv_mfma2_16(const uint8_t* __restrict__ Pa, int out_a,
@@ -415,6 +469,50 @@ hipError_t launch_matvec_mfma_nv(int kind, const void* P, int in_dim, int out_di
   if (kind == Q6_K) return nv <= 2 ? launch_mfma_nv_kind<Q6_K, 2>(w, in_dim, out_dim, nv, x, y, s)
                                    : launch_mfma_nv_kind<Q6_K, 4>(w, in_dim, out_dim, nv, x, y, s);
   return hipErrorNotSupported;
+}
+
+template <int KIND>
+static hipError_t launch_norm16_kind(const PackedPlan& p, const uint8_t* w, int in_dim, int out_dim, const float* H,
+                                     const float* r, const float* g, float* y, hipStream_t s) {
+  const dim3 grid((out_dim + 15) / 16);
+  const int nsb = in_dim / 256, pipe = mv_pipe(p);
+#define KQ_GO(N, PIPE)                                                                                      \
+  hipLaunchKernelGGL((kq_mv_mfma16_norm<KIND, N, PIPE>), grid, dim3(64 * N), 0, s, w, nsb, out_dim, H, r, g, y, \
+                     p.spw)
+#define KQ_NW(N)                                  \
+  case N:                                         \
+    if (pipe == MV_ONE) {                         \
+      KQ_GO(N, MV_ONE);                           \
+    } else if (pipe == MV_SEQ) {                  \
+      KQ_GO(N, MV_SEQ);                           \
+    } else {                                      \
+      KQ_GO(N, MV_PF);                            \
+    }                                             \
+    break;
+  switch (p.nw) {
+    KQ_NW(16) KQ_NW(14) KQ_NW(8) KQ_NW(4)
+    default: return hipErrorNotSupported;
+  }
+#undef KQ_NW
+#undef KQ_GO
+  return hipGetLastError();
+}
+
+bool matvec_norm_takes(int kind, int in_dim, int out_dim) {
+  if (!(kind == Q4_K || kind == Q6_K) || !matvec_mfma_takes(kind) || in_dim <= 0 || in_dim % 256 ||
+      in_dim > MV_NORM_MAX_DIM || out_dim <= 0)
+    return false;
+  const PackedPlan p = mfma_plan(kind, in_dim, out_dim);
+  return p.blk16 && p.nw >= 4 && p.nw != 2 && p.nw != 1;
+}
+
+hipError_t launch_matvec_norm(int kind, const void* P, int in_dim, int out_dim, const float* H, const float* r,
+                              const float* g, float* y, hipStream_t s) {
+  if (!matvec_norm_takes(kind, in_dim, out_dim)) return hipErrorNotSupported;
+  const PackedPlan p = mfma_plan(kind, in_dim, out_dim);
+  const uint8_t* w = (const uint8_t*)P;
+  return kind == Q4_K ? launch_norm16_kind<Q4_K>(p, w, in_dim, out_dim, H, r, g, y, s)
+                      : launch_norm16_kind<Q6_K>(p, w, in_dim, out_dim, H, r, g, y, s);
 }
 
 hipError_t launch_matvec_mfma(int kind, const void* P, int in_dim, int out_dim, const float* x, float* y, float* part,
