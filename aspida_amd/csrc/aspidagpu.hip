@@ -277,12 +277,22 @@ struct MvWorkspace {
 //   up to 4 vectors: the batch-1 kernel on 4 vectors where its batch-1
 //     plan is 16-row workgroups (and Q6_K at 2 vectors), else one pass;
 //   5-16 vectors: one pass;
+//   on matrices of at least MM16_TALL_UNITS pairs up to 16 vectors: the
+//     16-vector kernel (Q6_K up to 4 vectors: the batch-1 kernel on 4);
 //   above 16: one pass for Q6_K (launches of 32 vectors on 64-row tiles);
 //     Q4_K on the 64-vector kernel in one launch.
 // The 16-vector kernel stays an engine of its own (3).
 constexpr int MULTI_MAX_BATCH = 8;
 constexpr int MULTI_MAX_BATCH_MFMA_KINDS = 4;
 constexpr long MM16_MIN_UNITS = 2048;
+// From this many (64-row tile, super-block column) pairs, batches of up to 16
+// take the 16-vector kernel (Q4_K from 2 vectors, Q6_K from 5).  Measured on
+// MI355X, 8 vectors: Q6_K 151936x2048 98 against 129 us on the one-pass
+// kernel, 65536x2048 48 against 55, 32768x4096 45 against 55; Q4_K
+// 151936x2048 at 2 vectors 54 against 70, 65536x4096 45 against 47; below,
+// at 14336x4096 (3584 pairs), the one-pass kernel is ahead (Q4_K 8 vectors
+// 15.2 against 19.1 us).
+constexpr long MM16_TALL_UNITS = 8192;
 std::atomic<int> g_mm_engine{0};
 
 // The kernel family of a batched product and how many vectors each launch
@@ -308,10 +318,15 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   if (eng == 4 && kq::mmv_kind(kind)) return {3, 64};
   if (eng == 5 && kq::matvec_nv_takes(kind, in_dim, out_dim)) return {4, 4};
   if (eng == 0 && kq::mmv_kind(kind) && kq::matvec_nv_takes(kind, in_dim, out_dim)) {
+    // Very tall matrices (output heads): the 16-vector kernel, whose
+    // activation pre-pass is amortised over many rows.
+    const bool tall = units >= MM16_TALL_UNITS && kq::mm16_kind(kind);
     if (batch <= 4) {
+      if (tall) return kind == kq::Q6_K ? MmRoute{4, 4} : MmRoute{1, 16};
       if (kq::mfma_plan(kind, in_dim, out_dim).blk16 || (kind == kq::Q6_K && batch <= 2)) return {4, 4};
       return {3, 64};
     }
+    if (batch <= 16 && tall) return {1, 16};
     if (batch <= 16 || kind == kq::Q6_K) return {3, kq::mmv_step(kind, in_dim, out_dim)};
   }
   if (mm16) return {1, 16};

@@ -119,8 +119,7 @@ int moe_route_groups(int T);
 // The router with its input normalised in the same launch: x = RMSNorm(H +
 // r + r2) with weights g (r, r2 may be null; added in that order); the sum
 // is written back to H and x to nx.  Arguments otherwise as
-// launch_moe_route; dim <= 4096 and T below the many-token router's range
-// (moe_route_norm_takes).
+// launch_moe_route; dim <= 4096 and up to 2 tokens (moe_route_norm_takes).
 bool moe_route_norm_takes(int n_exp, int dim, int T, int top_k);
 hipError_t launch_moe_route_norm(const float* router_w, int n_exp, int dim, int T, int top_k, float* H, const float* r,
                                  const float* r2, const float* g, float* nx, float* logits, int* top_idx, float* top_w,

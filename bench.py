@@ -397,9 +397,14 @@ def small_batch_kernel(aa, kind, inp, out, B):
     4 vectors where the batch-1 plan is 16-row workgroups (and Q6_K at 2),
     else the one-pass kernel; the one-pass kernel up to 16 vectors and for
     Q6_K above; Q4_K above 16 on the 64-vector MFMA kernel."""
+    tall = (-(-out // 64)) * (inp // 256) >= 8192
     if B <= 4:
+        if tall:
+            return "kq_mv_mfma16n" if kind == aa.Q6_K else "kq_mm16_q4k"
         b16 = aa.DeviceOps().matvec_plan(kind, inp, out)[5]
         return "kq_mv_mfma16n" if b16 or (kind == aa.Q6_K and B <= 2) else "kq_mmv"
+    if B <= 16 and tall:
+        return "kq_mm16_q4k" if kind == aa.Q4_K else "kq_mm16_q6k"
     if B <= 16 or kind == aa.Q6_K:
         return "kq_mmv"
     return "kq_mm_mfma"

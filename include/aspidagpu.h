@@ -411,7 +411,9 @@ int aspida_kq_set_mv_engine(int engine);
  * (Q4_K and Q6_K: up to 4 vectors on the batch-1 matrix-core kernel where
  * the batch-1 plan is 16-row workgroups, else the one-pass kernel -- Q6_K
  * keeps the batch-1 kernel at 2 vectors -- then the one-pass kernel up to
- * 16 vectors; above 16 the one-pass kernel for Q6_K -- in launches of 32
+ * 16 vectors (on matrices of at least 8192 64-row-by-256-column blocks,
+ * such as output heads, the 16-vector matrix-core kernel instead, Q6_K from
+ * 5 vectors); above 16 the one-pass kernel for Q6_K -- in launches of 32
  * vectors where it takes 64-row tiles -- and the 64-vector matrix-core
  * kernel for Q4_K; other kinds on the vector kernel); 1 = the vector kernel; 2 = the 64-vector and 3 = the
  * 16-vector matrix-core kernel; 4 = the one-pass matrix-core kernel (up to

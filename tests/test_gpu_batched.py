@@ -176,7 +176,8 @@ def test_mfma_matmul_matches_oracle(kind, case):
 # one column per wave and long column runs, tiles split over workgroups.
 MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304), (40, 4096, 4096),
                    (9, 16448, 2048), (3, 256, 14336), (20, 12352, 512), (64, 12352, 256), (63, 300, 1024),
-                   (2, 13000, 256), (4, 12352, 512), (48, 12352, 512), (61, 13000, 256)]
+                   (2, 13000, 256), (4, 12352, 512), (48, 12352, 512), (61, 13000, 256),
+                   (5, 32768, 4096)]  # 8192 (tile, column) pairs: the pick's 16-vector kernel
 
 
 # Engine 4 is the one-pass kernel (kq_mmv.hip): 64-row tiles from 12352 rows
