@@ -615,11 +615,13 @@ def abi_path(aa, synth, seed, tokens=4):
             "note": "aspida_gpu_matvec with host buffers: per call H2D x, kernel, D2H y, synchronous"}
 
 
-def cpu_baseline(seed, threads):
+def cpu_baseline(seed, threads, check_gpu=None):
     """Aspida's CPU QMatVec (restated in C, pooled rows as LLM_Pool does) on the
     same decode stream, timed on a bounded sample: one layer's seven matvecs
     (139 MB of weights) and the output head, each the median of repeated runs;
-    tokens/s = 1 / (32 * layer + head)."""
+    tokens/s = 1 / (32 * layer + head).  With check_gpu = (torch, aa), the
+    same weights and activations also run once through the decode's five GPU
+    launch shapes and are checked against this QMatVec (gpu_spot_check)."""
     import numpy as np
     import oracle
     from aspida_amd import synth
@@ -650,12 +652,63 @@ def cpu_baseline(seed, threads):
     t_layer, n_layer = median_time(layer, 12.0)
     t_head, n_head = median_time(run_head, 6.0)
     t_tok = LAYERS * t_layer + t_head
-    return {"value": round(1.0 / t_tok, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+    parity = None
+    if check_gpu is not None:
+        named = {name: (kind, w) for (name, _, _, _), (kind, w, _, _) in zip(plan, ws)}
+        parity = gpu_spot_check(*check_gpu, named, head, xs, threads)
+    return {"value": round(1.0 / t_tok, 4), "unit": "tok/s", "cores": threads, "kind": "port", "parity": parity,
             "sample": (f"C restatement of QMatVec (llm_dequant.adb:808-932, llm_pool.adb:91-160), "
                        f"{threads} threads; one Llama-3-8B layer's 7 matvecs (median of {n_layer}) and the "
                        f"Q6_K head (median of {n_head}); token = 32*layer + head = {t_tok * 1e3:.1f} ms; "
                        f"{(LAYERS * sum(w.nbytes for _, w, _, _ in ws) + head.nbytes) / t_tok / 1e9:.2f} GB/s"),
             "cpu_model": _cpu_model()}
+
+
+def gpu_spot_check(torch, aa, named, head, xs, threads):
+    """Ties the timed decode launches to the oracle: the CPU baseline's own
+    Llama-3-8B layer and head, in the decode's launch shapes (q|k with v in one
+    two-matrix launch, o, gate|up, down, head; the same entry points and
+    therefore the same kernel picks as the timed token), computed once on the
+    GPU and compared per output with QMatVec (llm_dequant.adb:808-932):
+    |y - y_ref| <= 1e-4 * sum_i |w_i x_i|, ten times inside the 1e-3 bar.
+    Returns the largest err / sum|w x| per launch; exits if any is out."""
+    import numpy as np
+    import oracle
+    dev = aa.DeviceOps()
+    cat = lambda a, b: (named[a][0], np.concatenate([named[a][1], named[b][1]]))
+    mats = {"qk": cat("q", "k"), "v": named["v"], "o": named["o"], "gate_up": cat("gate", "up"),
+            "down": named["down"], "head": (Q6_K, head)}
+    dims = {"qk": (HIDDEN, HIDDEN + KV), "v": (HIDDEN, KV), "o": (HIDDEN, HIDDEN), "gate_up": (HIDDEN, 2 * FFN),
+            "down": (FFN, HIDDEN), "head": (HIDDEN, VOCAB)}
+    packed, ys = {}, {}
+    for name, (kind, w) in mats.items():
+        inp, out = dims[name]
+        raw = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+        packed[name] = torch.empty(dev.packed_bytes(kind, inp, out), dtype=torch.uint8, device="cuda")
+        dev.pack(kind, raw.data_ptr(), inp, out, packed[name].data_ptr())
+        ys[name] = torch.empty(out, dtype=torch.float32, device="cuda")
+    xd = {n: torch.from_numpy(np.ascontiguousarray(x)).cuda() for n, x in xs.items()}
+    torch.cuda.synchronize()
+    dev.matvec2_packed(Q4_K, packed["qk"].data_ptr(), HIDDEN + KV, ys["qk"].data_ptr(), Q6_K,
+                       packed["v"].data_ptr(), KV, ys["v"].data_ptr(), HIDDEN, xd[HIDDEN].data_ptr())
+    for name in ("o", "gate_up", "down", "head"):
+        kind, _ = mats[name]
+        inp, out = dims[name]
+        dev.matvec_packed(kind, packed[name].data_ptr(), inp, out, xd[inp].data_ptr(), ys[name].data_ptr())
+    torch.cuda.synchronize()
+    worst = {}
+    for name, (kind, w) in mats.items():
+        inp, out = dims[name]
+        want = oracle.qmatvec(kind, w, inp, out, xs[inp], nthreads=threads).astype(np.float64)
+        scale = np.abs(oracle.dequant(kind, w, inp, out)).astype(np.float64) @ np.abs(xs[inp].astype(np.float64))
+        err = np.abs(ys[name].cpu().numpy().astype(np.float64) - want) / np.maximum(scale, 1e-30)
+        worst[name] = float(err.max())
+        if not worst[name] <= 1e-4:
+            print(f"bench.py: GPU decode launch '{name}' differs from the oracle: max err/sum|wx| "
+                  f"{worst[name]:.3e} > 1e-4", file=sys.stderr, flush=True)
+            sys.exit(1)
+    return {"max_err_over_abs_dot": {k: float(f"{v:.3e}") for k, v in worst.items()}, "rtol": 1e-4,
+            "launches": "q|k+v, o, gate|up, down, head on the baseline's own weights"}
 
 
 def _cpu_model():
@@ -846,7 +899,7 @@ def main():
         host = host_cpus()
         threads = args.cpu_threads or min(16, host["allowed"] or 1)
         import oracle
-        base = cpu_baseline(args.seed, threads)
+        base = cpu_baseline(args.seed, threads, check_gpu=(torch, aa))
         builds = {"x86-64-v3": base["value"]}
         native = native_oracle()
         if native:
@@ -854,7 +907,7 @@ def main():
             nat = cpu_baseline(args.seed, threads)
             builds["native"] = nat["value"]
             if nat["value"] > base["value"]:
-                base = nat
+                base = {**nat, "parity": base["parity"]}
                 base["sample"] += "; oracle built -march=native on this host at run time"
         cpu = {**base, "builds": builds, "host": host}
         print(f"# CPU baseline: {builds} tok/s on {threads} threads of {host.get('cpus', host['nproc'])} "
