@@ -38,7 +38,7 @@ namespace kq {
 
 constexpr int MR_J = MOE_MFMA_JPW;  // jobs per chunk
 constexpr int MR_GC = 8;            // super-block columns whose images sit in LDS at once
-constexpr int MR_THREADS = 256;     // four waves: the 16-row blocks of a tile
+constexpr int MR_THREADS = 256;     // four waves: the 16-row blocks of a tile (HW = 1)
 
 // One activation image: the compact A image of one job's super-block
 // column, its sub-block sums, and 1/S.
@@ -77,20 +77,23 @@ __global__ __launch_bounds__(1024) void moe_plan_mf(MoeGroupedArgs a) {
 __device__ __forceinline__ void mr_clear(MrImg (&img)[MR_J][MR_GC]) {
   uint4* p = &img[0][0].q[0][0];
   constexpr int n = (int)(sizeof(MrImg) * MR_J * MR_GC / 16);
-  for (int i = threadIdx.x; i < n; i += MR_THREADS) p[i] = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // Image (jj, c) of columns g0 .. g0 + gc - 1 is built by wave (jj gc + c) % 4;
 // a wave builds at most MR_J * MR_GC / 4 of them.  The activations are
 // loaded first (mr_xload), the images built after the workgroup barrier
 // (mr_build).
+// With NWV = 8 waves (two halves), image (jj, c) is built by wave
+// (jj gc + c) % 8, at most MR_J * MR_GC / 8 per wave.
 constexpr int MR_BPW = MR_J * MR_GC / 4;
 
+template <int NWV = 4>
 __device__ __forceinline__ void mr_xload(float4 (&xv)[MR_BPW], const float* const (&src)[MR_J], int g0, int gc, int w,
                                          int lane) {
 #pragma unroll
-  for (int k = 0; k < MR_BPW; ++k) {
-    const int i = w + 4 * k;
+  for (int k = 0; k < MR_J * MR_GC / NWV; ++k) {
+    const int i = w + NWV * k;
     const int ii = i < MR_J * gc ? i : 0;  // past the group: a valid row, unused
     const int jj = ii / gc, c = ii - jj * gc;
     const float* row = jj == 0 ? src[0] : src[1];  // a select, not an indexed (scratch) array
@@ -98,12 +101,12 @@ __device__ __forceinline__ void mr_xload(float4 (&xv)[MR_BPW], const float* cons
   }
 }
 
-template <int KIND>
+template <int KIND, int NWV = 4>
 __device__ __forceinline__ void mr_build(MrImg (&img)[MR_J][MR_GC], const float4 (&xv)[MR_BPW], int gc, int nj,
                                          int w, int lane) {
 #pragma unroll
-  for (int k = 0; k < MR_BPW; ++k) {
-    const int i = w + 4 * k;
+  for (int k = 0; k < MR_J * MR_GC / NWV; ++k) {
+    const int i = w + NWV * k;
     if (i < nj * gc) {
       const int jj = i / gc, c = i - jj * gc;
       MrImg& m = img[jj][c];
@@ -256,8 +259,9 @@ __device__ __forceinline__ int mr_col(int s, int rot, int nsb) { return s + rot 
 
 // The combine launch's shared-expert gate g_t (one wave per token), spread
 // over the grid.
+template <int NWV>
 __device__ __forceinline__ void mr_housekeeping(const MoeGroupedArgs& a, int w, int lane) {
-  for (int t = blockIdx.x * 4 + w; t < a.T; t += gridDim.x * 4) {
+  for (int t = blockIdx.x * NWV + w; t < a.T; t += gridDim.x * NWV) {
     float s = 0.f;
     if (a.sgi) {
       const float4* g4 = reinterpret_cast<const float4*>(a.sgi);
@@ -278,13 +282,23 @@ __device__ __forceinline__ void mr_housekeeping(const MoeGroupedArgs& a, int w, 
 // The activation slices a step prefetches: the images of the group that
 // starts at the next step (`real`), or a repeat of slice 0 (cached) that
 // keeps every step's load count equal.
+template <int NWV>
 __device__ __forceinline__ void mr_xnext(float4 (&xv)[MR_BPW], const float* const (&src)[MR_J], bool real, int g0,
                                          int nsb, int w, int lane) {
-  mr_xload(xv, src, real ? g0 : 0, real ? std::min(MR_GC, nsb - g0) : 1, w, lane);
+  mr_xload<NWV>(xv, src, real ? g0 : 0, real ? std::min(MR_GC, nsb - g0) : 1, w, lane);
+}
+
+// The column after step s of this wave's half (mr_col order), or at the
+// unit's last step the next unit's first column of that half.
+template <int HW>
+__device__ __forceinline__ int mr_next_col(int s, bool last, int rot, int rotN, int nsb) {
+  const int hf = HW == 2 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) : 0;
+  return last ? mr_col(2 * hf, rotN, nsb) : mr_col(s + 2 * HW, rot, nsb);
 }
 
 template <int KIND>
 __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
+  constexpr int NWV = 4;
   __shared__ MrImg img[MR_J][MR_GC];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -296,7 +310,7 @@ __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
   const int4 C = mr_chunk(a, 1 + u / tiles);
   const int units = mr_chunk(a, 0).x * tiles;
   if (u >= units) {
-    mr_housekeeping(a, w, lane);
+    mr_housekeeping<NWV>(a, w, lane);
     return;
   }
   const auto gbase = [&](const MrUnit& V, const uint8_t* routed, const uint8_t* sh) {
@@ -308,7 +322,7 @@ __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
   // First the activations of the first group, then the weights: loads return
   // in order, so the images need not wait for the weights.
   float4 xv[MR_BPW];
-  mr_xload(xv, src, 0, std::min(MR_GC, nsb), w, lane);
+  mr_xload<NWV>(xv, src, 0, std::min(MR_GC, nsb), w, lane);
   const uint8_t* G = gbase(U, a.gate, a.sh_gate);
   const uint8_t* P = gbase(U, a.up, a.sh_up);
   int rot = mr_rot(U, nsb);
@@ -350,7 +364,7 @@ __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
         rotN = mr_rot(N, nsb);
       }
       const float* const xs[MR_J] = {last ? srcN[0] : src[0], last ? srcN[1] : src[1]};
-      mr_xnext(xv, xs, last || (s + 2) % MR_GC == 0, last ? 0 : s + 2, nsb, w, lane);
+      mr_xnext<NWV>(xv, xs, last || (s + 2) % MR_GC == 0, last ? 0 : s + 2, nsb, w, lane);
       const size_t off2 = (size_t)(last ? rotN : mr_col(s + 2, rot, nsb)) * GB;
       g0.load((last ? Gn : G) + off2, lane, w);
       u0.load((last ? Pn : P) + off2, lane, w);
@@ -374,16 +388,29 @@ __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
     P = Pn;
     rot = rotN;
   }
-  mr_housekeeping(a, w, lane);
+  mr_housekeeping<NWV>(a, w, lane);
 }
 
 // ---- down, then combine --------------------------------------------------------------
 
-template <int KIND>
-__global__ __launch_bounds__(MR_THREADS) void moe_down_mf(MoeGroupedArgs a) {
+// HW = 2 (eight waves): the tile's four 16-row blocks are each walked by two
+// waves, half hf taking the column steps s = 2 hf, 2 hf + 4, ... (two
+// columns per step), so a unit's columns are in flight twice as wide; the
+// halves meet in LDS (half 0's sum first) before yk is written.  Only for
+// 3..MR_GC columns (every half has a step, every image fits at once, built at
+// the unit's start); HW = 1 walks all columns in one wave per block.
+// Measured (Qwen3-MoE layer, down Q6_K 2048x768, so 3 columns): T = 32
+// 138.2/139.1 -> 134.7/136.8 us, T = 8 unchanged; the same split of the
+// gate/up launch (8 columns) measured T = 8 62.2 -> 67.6 us and is not used.
+
+template <int KIND, int HW>
+__global__ __launch_bounds__(MR_THREADS * HW) void moe_down_mf(MoeGroupedArgs a) {
+  constexpr int NWV = 4 * HW;
   __shared__ MrImg img[MR_J][MR_GC];
+  __shared__ float red[HW == 2 ? 4 * MR_J * 64 : 1];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wb = w & 3, hf = w >> 2;
   const int nsb = a.I / 256, tiles = a.tiles_dim;
   constexpr int GB = 64 * Block<KIND>::BYTES;
   int u = blockIdx.x;
@@ -397,11 +424,11 @@ __global__ __launch_bounds__(MR_THREADS) void moe_down_mf(MoeGroupedArgs a) {
   MrUnit U = mr_unit(C, u, tiles);
   const float* src[MR_J] = {hrow(U, 0), hrow(U, 1)};
   float4 xv[MR_BPW];
-  mr_xload(xv, src, 0, std::min(MR_GC, nsb), w, lane);
+  mr_xload<NWV>(xv, src, 0, std::min(MR_GC, nsb), w, lane);
   const uint8_t* D = dbase(U);
   int rot = mr_rot(U, nsb);
   MvCol<KIND, 1> d0, d1;
-  d0.load(D + (size_t)rot * GB, lane, w);
+  d0.load(D + (size_t)mr_col(2 * hf, rot, nsb) * GB, lane, wb);
   mr_clear(img);
   const MvLane L = mv_lane<KIND, 17>(img[0][0].q, lane);
   for (;;) {
@@ -414,10 +441,15 @@ __global__ __launch_bounds__(MR_THREADS) void moe_down_mf(MoeGroupedArgs a) {
     const uint8_t* Dn = D;
     int rotN = rot;
     float ad[MR_J] = {0.f, 0.f};
-    for (int s = 0; s < nsb; s += 2) {
-      const bool group = s % MR_GC == 0;
+    if (HW == 2) {
+      __syncthreads();
+      mr_build<KIND, NWV>(img, xv, nsb, U.two ? 2 : 1, w, lane);
+      __syncthreads();
+    }
+    for (int s = 2 * hf; s < nsb; s += 2 * HW) {
+      const bool group = HW == 1 && s % MR_GC == 0;
       const int c0 = mr_col(s, rot, nsb), c1 = mr_col(s + 1 < nsb ? s + 1 : s, rot, nsb);
-      d1.load(D + (size_t)c1 * GB, lane, w);
+      d1.load(D + (size_t)c1 * GB, lane, wb);
       if (group) {
         __syncthreads();
         mr_build<KIND>(img, xv, std::min(MR_GC, nsb - s), U.two ? 2 : 1, w, lane);
@@ -425,7 +457,7 @@ __global__ __launch_bounds__(MR_THREADS) void moe_down_mf(MoeGroupedArgs a) {
       }
       mr_dot<KIND>(d0, img, c0 % MR_GC, L, lane, U.two, ad);
       asm volatile("" ::: "memory");
-      const bool last = s + 2 >= nsb;
+      const bool last = s + 2 * HW >= nsb;
       if (last && more) {
         N = mr_unit(CN, un, tiles);
         srcN[0] = hrow(N, 0);
@@ -434,16 +466,22 @@ __global__ __launch_bounds__(MR_THREADS) void moe_down_mf(MoeGroupedArgs a) {
         rotN = mr_rot(N, nsb);
       }
       const float* const xs[MR_J] = {last ? srcN[0] : src[0], last ? srcN[1] : src[1]};
-      mr_xnext(xv, xs, last || (s + 2) % MR_GC == 0, last ? 0 : s + 2, nsb, w, lane);
-      d0.load(last ? Dn + (size_t)rotN * GB : D + (size_t)mr_col(s + 2, rot, nsb) * GB, lane, w);
+      mr_xnext<NWV>(xv, xs, last || (HW == 1 && (s + 2) % MR_GC == 0), last ? 0 : s + 2, nsb, w, lane);
+      d0.load((last ? Dn : D) + (size_t)mr_next_col<HW>(s, last, rot, rotN, nsb) * GB, lane, wb);
       if (s + 1 < nsb) mr_dot<KIND>(d1, img, c1 % MR_GC, L, lane, U.two, ad);
     }
     // yk of the unit's jobs; the combine launch after this one reads them.
-    const int row = U.tile * 64 + 16 * w + (lane & 15), q = lane >> 4;
+    const int row = U.tile * 64 + 16 * wb + (lane & 15), q = lane >> 4;
 #pragma unroll
     for (int jj = 0; jj < MR_J; ++jj) {
-      const float v = mr_rows(ad[jj], lane);
-      if (q == jj && (jj == 0 || U.two) && row < a.dim) a.yk[(size_t)U.job[jj] * a.dim + row] = v;
+      float v = mr_rows(ad[jj], lane);
+      if (HW == 2) {
+        float* r = red + (wb * MR_J + jj) * 64;
+        if (hf == 1) r[lane] = v;
+        __syncthreads();
+        if (hf == 0) v += r[lane];
+      }
+      if (hf == 0 && q == jj && (jj == 0 || U.two) && row < a.dim) a.yk[(size_t)U.job[jj] * a.dim + row] = v;
     }
     if (!more) break;
     u = un;
@@ -499,9 +537,30 @@ static int mmoe_resident(const void* kernel, int threads) {
 
 // Enough workgroups for every unit the schedule can produce (the chunk
 // bound times the tiles), at most what the device keeps resident at once.
-static int mr_grid(const MoeGroupedArgs& a, int tiles, const void* kernel) {
+static int mr_grid(const MoeGroupedArgs& a, int tiles, const void* kernel, int threads) {
   const long bound = (long)tiles * moe_max_chunks(a.T, a.top_k, std::min(a.n_exp, a.T * a.top_k), MR_J);
-  return (int)std::max<long>(1, std::min<long>(bound, mmoe_resident(kernel, MR_THREADS)));
+  return (int)std::max<long>(1, std::min<long>(bound, mmoe_resident(kernel, threads)));
+}
+
+// Two halves per 16-row block of the down launch where every half has a
+// column step and the images fit at once (moe_down_mf).
+static bool mr_halves(int nsb) { return nsb >= 3 && nsb <= MR_GC; }
+
+template <int KIND>
+static void launch_gate_up_mf(const MoeGroupedArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(moe_gate_up_mf<KIND>, dim3(mr_grid(a, a.I / 64, (const void*)moe_gate_up_mf<KIND>, MR_THREADS)),
+                     dim3(MR_THREADS), 0, s, a);
+}
+
+template <int KIND>
+static void launch_down_mf(const MoeGroupedArgs& a, hipStream_t s) {
+  const int tiles = a.tiles_dim;
+  if (mr_halves(a.I / 256))
+    hipLaunchKernelGGL((moe_down_mf<KIND, 2>), dim3(mr_grid(a, tiles, (const void*)moe_down_mf<KIND, 2>, 512)),
+                       dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((moe_down_mf<KIND, 1>), dim3(mr_grid(a, tiles, (const void*)moe_down_mf<KIND, 1>, 256)),
+                       dim3(256), 0, s, a);
 }
 
 bool moe_mfma_kind(int kind) { return kind == Q4_K || kind == Q6_K; }
@@ -509,10 +568,8 @@ bool moe_mfma_kind(int kind) { return kind == Q4_K || kind == Q6_K; }
 template <int GK, int DK>
 static hipError_t launch_mr(const MoeGroupedArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(moe_plan_mf, dim3(1), dim3(1024), 0, s, a);
-  hipLaunchKernelGGL(moe_gate_up_mf<GK>, dim3(mr_grid(a, a.I / 64, (const void*)moe_gate_up_mf<GK>)),
-                     dim3(MR_THREADS), 0, s, a);
-  hipLaunchKernelGGL(moe_down_mf<DK>, dim3(mr_grid(a, a.tiles_dim, (const void*)moe_down_mf<DK>)),
-                     dim3(MR_THREADS), 0, s, a);
+  launch_gate_up_mf<GK>(a, s);
+  launch_down_mf<DK>(a, s);
   hipLaunchKernelGGL(moe_combine_mf, dim3((a.dim + 255) / 256, a.T), dim3(256), 0, s, a);
   return hipGetLastError();
 }

@@ -293,6 +293,9 @@ PACKED_CASES = [
     (1792, 1792, 5, 2, aa.Q2_K, aa.Q8_0, False, 9),     # 7 columns: 1 wave x 7
     (256, 256, 3, 2, aa.Q6_K, aa.Q4_K, True, 130),      # one column; 87 jobs per expert
     (512, 768, 8, 4, aa.Q8_0, aa.Q5_K, True, 300),      # T * top_k > 1024: two launches
+    # matrix-core down with two halves per 16-row block (3..8 columns of inter)
+    (512, 2048, 16, 4, aa.Q4_K, aa.Q6_K, True, 24),     # 8 columns: two steps per half
+    (512, 1280, 16, 4, aa.Q6_K, aa.Q4_K, False, 12),    # 5 columns: half 0's second step has one
     # Q4_K / Q6_K from 96 tokens: the grouped prefill products (kq_moe_prefill.hip)
     (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 96),    # 16-job groups
     (1024, 512, 16, 2, aa.Q4_K, aa.Q6_K, True, 150),    # 16-job groups, ~19 jobs per expert
