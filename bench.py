@@ -109,7 +109,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--only", choices=["small", "moe", "kquant", "sweep", "decode70", "chain", "prefill"],
+    ap.add_argument("--only", choices=["small", "moe", "kquant", "sweep", "decode70", "chain", "prefill", "abi"],
                     help="run just this table (no decode line): for profiling one workload")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
@@ -836,6 +836,9 @@ def main():
     if args.only:
         if args.copy_probe_mib:
             copy_probe(torch, args.copy_probe_mib)
+        if args.only == "abi":
+            print(json.dumps({"abi_path": abi_path(aa, synth, args.seed)}), flush=True)
+            return
         if args.only == "chain":
             print(json.dumps({"moe_chain": moe_chain_table(aa, synth, args.seed)}), flush=True)
             return
