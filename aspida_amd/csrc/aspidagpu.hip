@@ -436,8 +436,9 @@ __global__ void stage_copy(const float4* __restrict__ src, float4* __restrict__ 
 
 // x -> device (through pinned staging), per-group sums (when `sums`), then
 // `launch`, then y <- device; synchronous.  With y_host the launch writes y
-// into the pinned buffer c.hy itself (kernels that store each output once),
-// so no device-to-host copy is queued.
+// into the pinned buffer c.hy itself (the matvec and small-batch kernels
+// store each output once, with plain stores), so no device-to-host copy is
+// queued.
 template <class F>
 int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int rows, bool sums, F&& launch,
              bool y_host = false) {
@@ -510,8 +511,8 @@ extern "C" void aspida_gpu_matmul(const void* w, long wbytes, int kind, int in_d
   if (!rc) rc = c.init() || c.ws.ensure(in_dim, out_dim, batch) ? -1 : 0;
   if (!rc)
     rc = run_host(c, x, (long)in_dim * batch, y, (long)out_dim * batch, in_dim, batch, false, [&]() {
-      return matmul_packed(kind, req.d, in_dim, out_dim, batch, c.dx.p, c.dy.p, c.ws, c.st);
-    });
+      return matmul_packed(kind, req.d, in_dim, out_dim, batch, c.dx.p, c.hy.p, c.ws, c.st);
+    }, true);
   if (rc) fill_nan(y, (long)out_dim * batch);
 }
 
