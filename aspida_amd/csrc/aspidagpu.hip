@@ -604,7 +604,12 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
     std::memcpy(c.hx.p + dim, top_w, (size_t)top_k * 4);
     std::memcpy(c.hx.p + dim + top_k, top_idx, (size_t)top_k * 4);
     if (gated) std::memcpy(c.hx.p + dim + 2 * top_k, shared_gate_inp, (size_t)dim * 4);
-    return check(hipMemcpyAsync(c.dh.p, c.hx.p, nstage * 4, hipMemcpyHostToDevice, c.st), "H2D");
+    // The stage is a whole number of float4s (64-float aligned; the pinned
+    // buffer is allocated to that length), copied by the GPU (stage_copy).
+    const int n4 = (int)(stage / 4);
+    hipLaunchKernelGGL(stage_copy, dim3(std::min(64, (n4 + 255) / 256)), dim3(256), 0, c.st, (const float4*)c.hx.p,
+                       (float4*)c.dh.p, n4);
+    return check(hipGetLastError(), "stage inputs");
   };
   std::shared_lock<std::shared_mutex> rd(g_wmu, std::defer_lock);
   // Grouped path over packed experts when gate, up and the shared gate/up
@@ -631,7 +636,7 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
     // The staged inputs, then the grouped work on a 256-byte boundary.
     const size_t scratch = stage + (kq::moe_grouped_work_bytes(1, dim, intermed, top_k) + 3) / 4;
     if (!rc && (c.init() || c.dy.ensure((size_t)dim, "hipMalloc y") || c.dh.ensure(scratch, "hipMalloc moe scratch") ||
-                c.hx.ensure(nstage, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
+                c.hx.ensure(stage, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
       rc = -1;
     if (!rc) {
       rc = stage_inputs();
@@ -673,7 +678,7 @@ extern "C" void aspida_gpu_moe_experts(const float* x, int dim, int top_k, int i
   const size_t front = std::max(stage, kq::moe_staging_floats(dim, 1, top_k));
   const size_t scratch = front + kq::moe_scratch_floats(mw, 1, top_k) - kq::moe_staging_floats(dim, 1, top_k);
   if (!rc && (c.init() || c.dy.ensure((size_t)dim, "hipMalloc y") || c.dh.ensure(scratch, "hipMalloc moe scratch") ||
-              c.hx.ensure(nstage, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
+              c.hx.ensure(stage, "pinned x") || c.hy.ensure((size_t)dim, "pinned y")))
     rc = -1;
   if (!rc) {
     rc = stage_inputs();
