@@ -76,22 +76,41 @@ __device__ __forceinline__ MvLane mv_lane(uint4 (&img)[8][IL], int lane) {
   return L;
 }
 
+// The bits of the largest |x| over the wave's float4s, in every lane.
+// Non-negative floats order as their bit patterns do, so the reduction is an
+// unsigned max on DPP-fused instructions; a NaN sorts above every finite
+// value (its column then takes S = 1; its outputs are NaN either way).
+__device__ __forceinline__ uint32_t wave_max_abs_bits(float4 v) {
+  uint32_t m = max(max(__builtin_bit_cast(uint32_t, v.x) & 0x7FFFFFFFu, __builtin_bit_cast(uint32_t, v.y) & 0x7FFFFFFFu),
+                   max(__builtin_bit_cast(uint32_t, v.z) & 0x7FFFFFFFu, __builtin_bit_cast(uint32_t, v.w) & 0x7FFFFFFFu));
+  auto step = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x111, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x112, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x114, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x118, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x142, 0xA, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x143, 0xC, 0xF, true));
+  return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
+}
+
 // Builds the column's A image and sub-block sums of x S from the lane's
-// float4 of x; returns 1/S.
+// float4 of x; returns 1/S.  S = 2^se puts the column's largest |x| just below
+// 2^14: se = 14 - e for max |x| = f 2^e, f in [0.5, 1), i.e. 140 minus its
+// biased exponent, at most 120 (0 for an all-zero column or a non-finite
+// maximum).  The exponent arithmetic is wave-uniform (scalar instructions).
 template <int KIND>
 __device__ __forceinline__ float build_image(float4 xv, const MvLane& L, float* xsum) {
-  float mx = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
-  mx = wave_max(mx);
-  int e = 0;
-  const bool scaled = mx > 0.f && __builtin_isfinite(mx);
-  if (scaled) (void)frexpf(mx, &e);
-  const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
-  const float S = ldexpf(1.f, se);
+  const uint32_t mx = wave_max_abs_bits(xv);
+  const int se = (mx == 0u || mx >= 0x7F800000u) ? 0 : std::min(140 - (int)(mx >> 23), 120);
+  const float S = __builtin_bit_cast(float, (uint32_t)(se + 127) << 23);
   const float sl = S * L.odd;
   const float v0 = xv.x * sl, v1 = xv.y * sl, v2 = xv.z * sl, v3 = xv.w * sl;
   const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1, h2 = (_Float16)v2, h3 = (_Float16)v3;
   // lo is stored times 2^11 (exact: a power of two), so that its products
-  // stay as large as hi's inside the matrix cores' sums.
+  // stay as large as hi's inside the matrix cores' sums.  (Written with the
+  // scalar conversions: the same arithmetic through gfx950's packed
+  // v_cvt_pk_f16_f32 gave NaN outputs in the grouped MoE kernels on MI355X,
+  // cause not identified.)
   const _Float16 l0 = (_Float16)((v0 - (float)h0) * 2048.f), l1 = (_Float16)((v1 - (float)h1) * 2048.f);
   const _Float16 l2 = (_Float16)((v2 - (float)h2) * 2048.f), l3 = (_Float16)((v3 - (float)h3) * 2048.f);
   float su = (xv.x + xv.y) + (xv.z + xv.w);
@@ -101,7 +120,7 @@ __device__ __forceinline__ float build_image(float4 xv, const MvLane& L, float* 
   *reinterpret_cast<uint2*>(L.wr_hi) = make_uint2(pack_f16x2(h0, h2), pack_f16x2(h1, h3));
   *reinterpret_cast<uint2*>(L.wr_hi + 4) = make_uint2(pack_f16x2(l0, l2), pack_f16x2(l1, l3));
   if (L.xs_writer) xsum[L.xs_pos] = su * S;
-  return ldexpf(1.f, -se);
+  return __builtin_bit_cast(float, (uint32_t)(127 - se) << 23);
 }
 
 // One super-block column of RB 16-row blocks (RB = 4: the whole 64-row tile;

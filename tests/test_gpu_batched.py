@@ -329,7 +329,8 @@ def test_reference_harness_against_this_library():
     1e-2) and batched == per-row (rel < 1e-4)."""
     exe = os.path.join(os.path.dirname(oracle.__file__), "_ref", "test_matvec")
     if not os.path.exists(exe):
-        pytest.skip("oracle/_ref/test_matvec not built (reference tree absent at build time)")
+        pytest.skip("oracle/_ref/test_matvec absent: it is built only where the reference tree is mounted, and "
+                    "no reference build output travels to a GPU box")
     torch_cuda()
     r = subprocess.run([exe], cwd=os.path.dirname(aa.LIB_PATH), capture_output=True, text=True, timeout=600)
     print(r.stdout[-3000:])
