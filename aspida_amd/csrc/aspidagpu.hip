@@ -196,15 +196,19 @@ int acquire(std::shared_lock<std::shared_mutex>& rd, WReq* r, int n) {
 
 // ---- per-thread execution context -------------------------------------------
 
-// Device buffer that only grows, and never frees a buffer it has handed out:
-// a HIP graph captured while an older, smaller buffer was current keeps its
-// pointer, so a later growth must leave that memory valid.  Growth at least
-// doubles, so the superseded buffers together stay smaller than the current
-// one; all of them live until the process ends.
+// Device buffer that only grows.  By default it never frees a buffer it has
+// handed out: a HIP graph captured while an older, smaller buffer was current
+// keeps its pointer, so a later growth must leave that memory valid.  Growth
+// at least doubles, so the superseded buffers together stay smaller than the
+// current one; all of them live until the process ends.  Buffers that no
+// graph can hold (the host ABI's per-thread ones, used only inside a call
+// that ends with a stream synchronisation) set keep_old = false and free the
+// superseded buffer when they grow.
 template <class T>
 struct DevBuf {
   T* p = nullptr;
   size_t n = 0;
+  bool keep_old = true;
   std::vector<T*> old;
   // 0 or -1; *grew says whether p is a new, uninitialised buffer.
   int ensure(size_t want, const char* what, bool* grew = nullptr) {
@@ -213,7 +217,8 @@ struct DevBuf {
     const size_t sz = std::max(want, 2 * n);
     T* q = nullptr;
     if (check(hipMalloc(&q, sz * sizeof(T)), what)) return -1;
-    if (p) old.push_back(p);
+    if (p && keep_old) old.push_back(p);
+    else if (p) (void)hipFree(p);
     p = q;
     n = sz;
     if (grew) *grew = true;
@@ -293,7 +298,9 @@ constexpr long MM16_MIN_UNITS = 2048;
 // at 14336x4096 (3584 pairs), the one-pass kernel is ahead (Q4_K 8 vectors
 // 15.2 against 19.1 us).
 constexpr long MM16_TALL_UNITS = 8192;
-std::atomic<int> g_mm_engine{0};
+// Test and tuning overrides (aspida_kq_set_*) are per calling thread: a
+// thread's override changes only the launches that thread makes.
+thread_local int g_mm_engine = 0;
 
 // The kernel family of a batched product and how many vectors each launch
 // takes: 0 the multi-vector VALU kernel, 1 the 16-vector and 2 the 64-vector
@@ -302,7 +309,7 @@ struct MmRoute {
   int family, step;
 };
 MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
-  const int eng = g_mm_engine.load(std::memory_order_relaxed);
+  const int eng = g_mm_engine;
   const long units = (long)((out_dim + 63) / 64) * (in_dim / 256);
   // Q4_K above 16 vectors: one pass of the 64-vector kernel rather than 16
   // vectors per launch (14336x4096: 32 vectors 37 -> 31 us, 64 vectors
@@ -379,6 +386,12 @@ struct Ctx {
   HostBuf<float> hx, hy;
   DevBuf<int> di;
   MvWorkspace ws;
+  // Every call on this context ends with hipStreamSynchronize and none is
+  // captured into a graph, so a superseded buffer is idle when it is freed.
+  Ctx() {
+    dx.keep_old = dy.keep_old = dq.keep_old = dh.keep_old = di.keep_old = false;
+    ws.part.keep_old = ws.count.keep_old = ws.mm.keep_old = false;
+  }
   int init() {
     if (st) return 0;
     return check(hipStreamCreateWithFlags(&st, hipStreamNonBlocking), "hipStreamCreate");
@@ -390,13 +403,11 @@ Ctx& ctx() {
   return *c;
 }
 
-// Launch-shape override for batch-1 matvecs (tuning and tests); rows <= 0
-// means "use kq::default_mv_config".
-std::mutex g_cfg_mu;
-int g_cfg_rows = 0, g_cfg_wpc = 16;
+// Launch-shape override for batch-1 matvecs (tuning and tests, per calling
+// thread); rows <= 0 means "use kq::default_mv_config".
+thread_local int g_cfg_rows = 0, g_cfg_wpc = 16;
 
 kq::MvConfig mv_config(int kind, int in_dim, int out_dim) {
-  std::lock_guard<std::mutex> lk(g_cfg_mu);
   if (g_cfg_rows <= 0) return kq::default_mv_config(kind, in_dim, out_dim);
   kq::MvConfig c;
   c.rows_per_wave = g_cfg_rows;
@@ -443,7 +454,7 @@ template <class F>
 int run_host(Ctx& c, const float* x, long nx, float* y, long ny, int in_dim, int rows, bool sums, F&& launch,
              bool y_host = false) {
   if (c.init()) return -1;
-  if (c.dx.ensure((size_t)nx, "hipMalloc x") || c.dy.ensure((size_t)ny, "hipMalloc y") ||
+  if (c.dx.ensure((size_t)nx, "hipMalloc x") || (!y_host && c.dy.ensure((size_t)ny, "hipMalloc y")) ||
       c.dq.ensure((size_t)(nx / 16 + 1), "hipMalloc xsum") || c.hx.ensure((size_t)nx, "pinned x") ||
       c.hy.ensure((size_t)ny, "pinned y"))
     return -1;
@@ -1055,9 +1066,13 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
                   kq::moe_grouped_experts_ok(n_exp) &&
                   ((uintptr_t)x & 15) == 0 && ((uintptr_t)work & 255) == 0;
   if (!ok) return -EINVAL;
-  // An error left by earlier work on this thread is reported as such, not as this call's.
-  if (const hipError_t pend = hipGetLastError(); pend != hipSuccess)
+  // An error left pending by earlier work on this thread is returned (and
+  // recorded) as such before anything is launched: the call does no work, and
+  // its return code and aspida_gpu_last_error agree.
+  if (const hipError_t pend = hipGetLastError(); pend != hipSuccess) {
     report((int)pend, "aspida_moe_experts_packed_dev: error pending from earlier work: %s", hipGetErrorString(pend));
+    return (int)pend;
+  }
   kq::MoeGroupedArgs a{};
   a.gate = (const uint8_t*)gate_p; a.up = (const uint8_t*)up_p; a.down = (const uint8_t*)down_p;
   a.sh_gate = (const uint8_t*)shg_p; a.sh_up = (const uint8_t*)shu_p; a.sh_down = (const uint8_t*)shd_p;
@@ -1171,14 +1186,13 @@ extern "C" int aspida_kq_set_mv_engine(int engine) {
 
 extern "C" int aspida_kq_set_mm_engine(int engine) {
   if (engine < 0 || engine > 5) return -EINVAL;
-  g_mm_engine.store(engine, std::memory_order_relaxed);
+  g_mm_engine = engine;
   return 0;
 }
 
 extern "C" int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu) {
   if (rows_per_wave > 0 && !(rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4)) return -EINVAL;
   if (rows_per_wave > 0 && (waves_per_cu < 1 || waves_per_cu > 64)) return -EINVAL;
-  std::lock_guard<std::mutex> lk(g_cfg_mu);
   g_cfg_rows = rows_per_wave;
   g_cfg_wpc = waves_per_cu;
   return 0;

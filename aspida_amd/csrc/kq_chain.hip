@@ -37,6 +37,7 @@
 #include <vector>
 
 #include "kq_chain.h"
+#include "kq_host.h"
 #include "kq_kernels.h"
 #include "kq_packed.h"
 
@@ -249,14 +250,15 @@ static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
 }
 
 static int chain_grid() {
-  int dev = 0, cus = 0, per = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)kq_chain, 64 * CH_NW, 0) != hipSuccess ||
-      per <= 0)
-    per = 1;  // fewer workgroups than fit: still all resident
-  (void)hipGetLastError();
+  int dev = 0, cus = 256, per = 1;
+  (void)query_clean([&] {
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)kq_chain, 64 * CH_NW, 0) != hipSuccess ||
+        per <= 0)
+      per = 1;  // fewer workgroups than fit: still all resident
+  });
   const int G = per * cus / CH_EPOCH_CTRS * CH_EPOCH_CTRS;
   return G > 0 ? G : CH_EPOCH_CTRS;
 }

@@ -53,7 +53,7 @@ void set_mfma_rows(int mode);
 // Tuning: 0 = the plan's choice, 1 = prefetching waves, 2 = sequential columns
 // (for splits with more than one column per wave).
 void set_mfma_pipeline(int mode);
-// Process-wide override of packed_plan for tuning (nw a power of two <= 16,
+// Per-thread override of packed_plan for tuning (nw a power of two <= 16,
 // nw * ks dividing in_dim / 256; anything else, or 0, restores the choice).
 void set_packed_plan_override(int nw, int ks);
 // The override's workgroups per tile (0: none); the small-batch MFMA product

@@ -28,6 +28,7 @@
 // sums are the matrix cores' f32 sums in another order than the CPU's.
 #include <algorithm>
 
+#include "kq_host.h"
 #include "kq_kernels.h"
 #include "kq_mv_mfma.h"
 
@@ -452,15 +453,16 @@ struct MmvPlan {
   int rb, nw, spw;
 };
 static int mmv_cus() {
-  static const int cus = [] {
-    int dev = 0, c = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        c <= 0)
-      c = 256;
-    (void)hipGetLastError();
-    return c;
-  }();
-  return cus;
+  static OnceQuery<int> q;
+  return q.get(
+      [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+          c = 256;
+        return c;
+      },
+      256);
 }
 static MmvPlan mmv_plan(int kind, int in_dim, int out_dim, int ng) {
   const int nsb = in_dim / 256, tiles = (out_dim + 63) / 64;

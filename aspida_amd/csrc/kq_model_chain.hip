@@ -402,6 +402,10 @@ int ensure_bufs(Chain& c) {
 
 void free_all(Chain& c) {
   drop_run_state(c);
+  // A new registration starts with no lane count run eagerly, so that the
+  // first forward of every lane count sizes the workspaces again before a
+  // graph is captured (forward()).
+  c.warmed.clear();
   for (void* p : c.mem) (void)hipFree(p);
   c.mem.clear();
   c.layers.clear();

@@ -27,6 +27,7 @@
 #include <map>
 #include <mutex>
 
+#include "kq_host.h"
 #include "kq_kernels.h"
 #include "kq_moe.h"
 #include "kq_moe_sched.h"
@@ -340,18 +341,22 @@ static int moe_resident(const void* kernel, int threads) {
   static std::mutex mu;
   static std::map<std::pair<const void*, int>, int> cache;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipPeekAtLastError() != hipSuccess || hipGetDevice(&dev) != hipSuccess) return 256;
   std::lock_guard<std::mutex> lk(mu);
   auto it = cache.find({kernel, dev});
   if (it != cache.end()) return it->second;
   int cus = 0, per = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  // The query fails ("unknown error") for some kernels of 256 VGPRs on this
-  // runtime, the Q8_0 grouped ones among them; their launches are fine.  Then
-  // one resident workgroup per CU is assumed, and the query's error is cleared
-  // so that the launch's own check does not report it.
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
-  (void)hipGetLastError();
+  // The occupancy query fails ("unknown error") for some kernels of 256 VGPRs
+  // on this runtime, the Q8_0 grouped ones among them; their launches are
+  // fine.  Then one resident workgroup per CU is assumed, and the query's own
+  // error is cleared (query_clean, kq_host.h) so that the launch's check does
+  // not report it; an error pending from earlier work is left in place.
+  if (!query_clean([&] {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+          cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
+      }))
+    return 256;
   return cache[{kernel, dev}] = per * cus;
 }
 

@@ -29,6 +29,7 @@
 #include <map>
 #include <mutex>
 
+#include "kq_host.h"
 #include "kq_kernels.h"
 #include "kq_moe.h"
 #include "kq_moe_sched.h"
@@ -520,18 +521,24 @@ __global__ __launch_bounds__(256) void moe_combine_mf(MoeGroupedArgs a) {
 
 // ---- launchers ------------------------------------------------------------------
 
+// Resident workgroups of a kernel on the current device (per CU times CUs),
+// cached per (kernel, device) once the queries ran cleanly (kq_host.h); 256
+// while an error from earlier work on this thread is pending.
 static int mmoe_resident(const void* kernel, int threads) {
   static std::mutex mu;
   static std::map<std::pair<const void*, int>, int> cache;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipPeekAtLastError() != hipSuccess || hipGetDevice(&dev) != hipSuccess) return 256;
   std::lock_guard<std::mutex> lk(mu);
   auto it = cache.find({kernel, dev});
   if (it != cache.end()) return it->second;
   int cus = 0, per = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
-  (void)hipGetLastError();
+  if (!query_clean([&] {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+          cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess || per <= 0) per = 1;
+      }))
+    return 256;
   return cache[{kernel, dev}] = per * cus;
 }
 

@@ -50,6 +50,7 @@
 #include <algorithm>
 #include <atomic>
 
+#include "kq_host.h"
 #include "kq_kernels.h"
 #include "kq_mv_mfma.h"
 
@@ -235,12 +236,13 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma16n(const uint8_t* __restri
 }
 
 // 0: the MFMA kernel for Q4_K and Q6_K, 1: the VALU kernel (comparison and tuning).
-static std::atomic<int> g_engine{0};
+// Per calling thread (a test or tuning override).
+static thread_local int g_engine = 0;
 
 void set_matvec_engine(int engine) { g_engine = engine; }
 
 bool matvec_mfma_takes(int kind) {
-  return (kind == Q4_K || kind == Q6_K || kind == Q2_K || kind == Q5_K || kind == Q3_K) && g_engine.load() == 0;
+  return (kind == Q4_K || kind == Q6_K || kind == Q2_K || kind == Q5_K || kind == Q3_K) && g_engine == 0;
 }
 
 // The kernel a plan runs: NW waves per workgroup and the column walk.
@@ -258,7 +260,8 @@ struct LdsRoom {
 };
 
 // min_static: the kernel's static LDS as this file lays it out, a floor in
-// case the runtime reports less; 1 KB of the limit is left unused.
+// case the runtime reports less; 1 KB of the limit is left unused.  Run
+// through OnceQuery (kq_host.h), which clears the error a failed query leaves.
 static LdsRoom lds_room_of(const void* kernel, size_t min_static) {
   LdsRoom r;
   hipFuncAttributes fa;
@@ -273,30 +276,31 @@ static LdsRoom lds_room_of(const void* kernel, size_t min_static) {
       r.dyn_max = (size_t)smem - stat - 1024;
     }
   }
-  (void)hipGetLastError();
   return r;
 }
 
 // One per kernel (K is the kernel itself, so each instantiation has its own).
 template <auto K, int NW>
 static LdsRoom lds_room() {
-  static const LdsRoom r =
-      lds_room_of(reinterpret_cast<const void*>(K), (size_t)NW * (sizeof(MvShared16) + 16 * sizeof(float)));
-  return r;
+  static OnceQuery<LdsRoom> q;
+  return q.get(
+      [] { return lds_room_of(reinterpret_cast<const void*>(K), (size_t)NW * (sizeof(MvShared16) + 16 * sizeof(float))); },
+      LdsRoom{});
 }
 
 static int device_attr(hipDeviceAttribute_t a, int fallback) {
   int dev = 0, v = 0;
   const bool ok = hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, a, dev) == hipSuccess && v > 0;
-  (void)hipGetLastError();
   return ok ? v : fallback;
 }
 
 // Never more than the kernel's own dynamic allowance (room.dyn_max), so static
 // plus dynamic LDS stays within the per-workgroup limit.
 static size_t mv16_spread_lds(int blocks, const LdsRoom& room) {
-  static const int cus = device_attr(hipDeviceAttributeMultiprocessorCount, 256);
-  static const int lds_cu = device_attr(hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, 160 * 1024);
+  static OnceQuery<int> qc, ql;
+  const int cus = qc.get([] { return device_attr(hipDeviceAttributeMultiprocessorCount, 256); }, 256);
+  const int lds_cu =
+      ql.get([] { return device_attr(hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, 160 * 1024); }, 160 * 1024);
   const size_t per_cu = std::max<size_t>(1, ((size_t)blocks + cus - 1) / cus);
   const size_t share = (size_t)lds_cu / per_cu, need = room.stat + 2048;
   if (share <= need) return 0;

@@ -142,9 +142,10 @@ static int pow2_divisor_upto(int n, int cap) {
   return d;
 }
 
-// Process-wide override of the split (tuning): waves per workgroup and
+// Per-thread override of the split (tuning): waves per workgroup and
 // workgroups per tile, 0 = the built-in choice.
-static std::atomic<int> g_plan_nw{0}, g_plan_ks{0};
+// Test and tuning overrides, per calling thread.
+static thread_local int g_plan_nw = 0, g_plan_ks = 0;
 
 void set_packed_plan_override(int nw, int ks) {
   g_plan_nw = nw;
@@ -214,11 +215,11 @@ PackedPlan packed_plan(int in_dim, int out_dim) {
 //     (<= 8) that still leave >= 150 workgroups, at least 2 (4096x14336 Q6_K
 //     8 x 7 groups: 12.6 us against 14.1 for 4 x 14; 4096x4096: 4 x 4, 5.5 us;
 //     1024x4096: 2 x 8).
-static std::atomic<int> g_mfma_pipe{0};
+static thread_local int g_mfma_pipe = 0;
 
 void set_mfma_pipeline(int mode) { g_mfma_pipe = mode; }
 
-static std::atomic<int> g_mfma_rows{0};
+static thread_local int g_mfma_rows = 0;
 
 void set_mfma_rows(int mode) { g_mfma_rows = mode; }
 

@@ -612,7 +612,9 @@ def abi_path(aa, synth, seed, tokens=4):
     return {"decode_8b": {"tok_s": round(1 / t_tok, 2), "ms_per_token": round(t_tok * 1e3, 3),
                           "calls_per_token": calls, "tokens": tokens},
             "kquant_matvec": per_kind,
-            "note": "aspida_gpu_matvec with host buffers: per call H2D x, kernel, D2H y, synchronous"}
+            "note": ("aspida_gpu_matvec with host buffers, synchronous: per call x is copied into pinned memory and "
+                     "staged to HBM by a copy kernel that reads it, the matvec writes y straight into pinned host "
+                     "memory, then the stream is synchronised (no copy-engine transfer per call)")}
 
 
 def cpu_baseline(seed, threads, check_gpu=None):

@@ -381,9 +381,10 @@ int aspida_gguf_tensor(const aspida_gguf *g, long long i, aspida_gguf_tensor_inf
 long long aspida_gguf_read(const aspida_gguf *g, long long i, void *dst, long long cap);
 
 /* ---- test and tuning hooks (no reference counterpart) ----------------------
- * The aspida_kq_set_* overrides below change process-wide state that every
- * thread's next launch reads: call them only while no other thread is calling
- * the library (tests, tuning runs), never from production callers. */
+ * The aspida_kq_set_* overrides below are per calling thread: each changes
+ * the kernel choice of the launches the calling thread makes from then on,
+ * and no other thread's.  They exist for tests and tuning runs; production
+ * callers leave them at their defaults. */
 
 /* Small-batch workspace check, host only (launches nothing): the bytes of
  * activation split and partial sums the library allocates for a batched
@@ -395,14 +396,14 @@ int aspida_kq_matmul_workspace(int kind, int in_dim, int out_dim, int batch, lon
 /* Split override for the packed kernels (aspida_kq_packed_plan): waves per
  * workgroup (a power of two <= 16) and workgroups per tile, applied to every
  * shape whose in_dim / 256 they divide; 0, 0 restores the built-in choice.
- * Process-wide; for tuning and tests. */
+ * Per calling thread; for tuning and tests. */
 int aspida_kq_set_packed_plan(int waves_per_group, int groups_per_tile);
 
 /* Engine of the batch-1 packed matvec (aspida_kq_matvec_packed_dev and the
  * calls built on it): 0 = matrix cores (MFMA) for Q4_K and Q6_K, the vector
  * kernel for the other kinds (the default); 1 = the vector kernel for every
  * kind.
- * Process-wide; for comparison and tests.  No reference counterpart.
+ * Per calling thread; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mv_engine(int engine);
 
@@ -420,26 +421,26 @@ int aspida_kq_set_mv_engine(int engine);
  * 64 vectors per weight pass); 5 = the batch-1 matrix-core kernel on up to 4
  * vectors per launch; for the kinds that have one (others stay on the
  * vector kernel).
- * Process-wide; for comparison and tests.  No reference counterpart.
+ * Per calling thread; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mm_engine(int engine);
 
 /* Workgroup shape of the matrix-core matvec: 0 = the built-in choice (16-row
  * workgroups over all columns for matrices of up to two such blocks per
  * compute unit, 64-row workgroups above), 1 = 64-row, 2 = 16-row workgroups.
- * Process-wide; for tuning and tests.  No reference counterpart.
+ * Per calling thread; for tuning and tests.  No reference counterpart.
  * Returns 0 or -EINVAL. */
 int aspida_kq_set_mfma_rows(int mode);
 
 /* Tuning of the matrix-core matvec's splits with several columns per wave:
  * 0 = the built-in choice, 1 = prefetching waves (two register sets),
  * 2 = columns one after another (one register set, more waves per CU).
- * Process-wide.  No reference counterpart.  Returns 0 or -EINVAL. */
+ * Per calling thread.  No reference counterpart.  Returns 0 or -EINVAL. */
 int aspida_kq_set_mfma_pipeline(int mode);
 
 /* Launch-shape override for batch-1 matvecs: rows per lane group per step
  * (1, 2 or 4) and resident waves launched per CU (1..64); rows_per_wave <= 0
- * restores the built-in choice.  Process-wide; for tuning and tests. */
+ * restores the built-in choice.  Per calling thread; for tuning and tests. */
 int aspida_kq_set_mv_config(int rows_per_wave, int waves_per_cu);
 
 #ifdef __cplusplus

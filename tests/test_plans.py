@@ -55,3 +55,25 @@ def test_vector_engine_switch_leaves_the_matrix_cores(dev):
     finally:
         dev.set_mv_engine(0)
     assert dev.matvec_plan(aa.Q4_K, 4096, 4096)[0]
+
+
+def test_overrides_are_per_thread(dev):
+    """The aspida_kq_set_* overrides change only the calling thread's launches:
+    a thread that forces 64-row workgroups and the vector engine sees its own
+    plans change, while this thread keeps the built-in ones."""
+    import threading
+
+    seen = {}
+
+    def other():
+        dev.set_mfma_rows(1)
+        seen["rows"] = dev.matvec_plan(aa.Q4_K, 4096, 4096)
+        dev.set_mv_engine(1)
+        seen["engine"] = dev.matvec_plan(aa.Q4_K, 4096, 4096)[0]
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["rows"][5] is False and seen["rows"][0]   # 64-row workgroups in that thread
+    assert seen["engine"] is False                         # vector engine in that thread
+    assert dev.matvec_plan(aa.Q4_K, 4096, 4096) == (True, 16, 1, 1, False, True)  # untouched here
