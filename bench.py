@@ -109,8 +109,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--only", choices=["small", "moe", "kquant", "sweep", "decode70", "chain", "prefill", "abi"],
-                    help="run just this table (no decode line): for profiling one workload")
+    ap.add_argument("--only", choices=["small", "moe", "kquant", "sweep", "decode70", "chain", "prefill", "abi",
+                                       "resident"],
+                    help="run just this table (no decode line): for profiling one workload; 'resident' times "
+                         "the persistent matvec chain experiment beside the decode")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
     ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B weight-stream line")
@@ -658,6 +660,8 @@ def cpu_baseline(seed, threads, check_gpu=None):
     if check_gpu is not None:
         named = {name: (kind, w) for (name, _, _, _), (kind, w, _, _) in zip(plan, ws)}
         parity = gpu_spot_check(*check_gpu, named, head, xs, threads)
+        parity["small_batch"] = small_batch_spot_check(*check_gpu, named, gen, threads)
+        parity["moe_layer"] = moe_spot_check(*check_gpu, gen, threads)
     return {"value": round(1.0 / t_tok, 4), "unit": "tok/s", "cores": threads, "kind": "port", "parity": parity,
             "sample": (f"C restatement of QMatVec (llm_dequant.adb:808-932, llm_pool.adb:91-160), "
                        f"{threads} threads; one Llama-3-8B layer's 7 matvecs (median of {n_layer}) and the "
@@ -711,6 +715,117 @@ def gpu_spot_check(torch, aa, named, head, xs, threads):
             sys.exit(1)
     return {"max_err_over_abs_dot": {k: float(f"{v:.3e}") for k, v in worst.items()}, "rtol": 1e-4,
             "launches": "q|k+v, o, gate|up, down, head on the baseline's own weights"}
+
+
+def small_batch_spot_check(torch, aa, named, gen, threads):
+    """Ties the small_batch table's kernels to the oracle: each small-batch
+    kernel family the library picks at the table's shapes (small_batch_kernel)
+    runs once through the same entry point (aspida_kq_matmul_packed_dev) --
+    Q4_K 4096 x 4096 (the baseline's own o) at B = 2, 8 and 64, and a Q6_K
+    14336 x 4096 matrix at B = 2, 16 and 64 -- and 64 sampled rows of every
+    vector's output are compared with QMatVec (llm_dequant.adb:808-932) within
+    1e-4 * sum_i |w_i x_i|.  Exits if any is out."""
+    import numpy as np
+    import oracle
+    from aspida_amd import synth
+    dev = aa.DeviceOps()
+    q6 = synth.weight_np(Q6_K, FFN, HIDDEN, gen)
+    cases = [(Q4_K, named["o"][1], HIDDEN, HIDDEN, b) for b in (2, 8, 64)] + \
+            [(Q6_K, q6, FFN, HIDDEN, b) for b in (2, 16, 64)]
+    worst = {}
+    for kind, w, out, inp, B in cases:
+        raw = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+        P = torch.empty(dev.packed_bytes(kind, inp, out), dtype=torch.uint8, device="cuda")
+        dev.pack(kind, raw.data_ptr(), inp, out, P.data_ptr())
+        X = synth.activations_np(B * inp, gen).reshape(B, inp)
+        xd = torch.from_numpy(X).cuda()
+        yd = torch.full((B, out), float("nan"), device="cuda")
+        torch.cuda.synchronize()
+        dev.matmul_packed(kind, P.data_ptr(), inp, out, B, xd.data_ptr(), yd.data_ptr())
+        torch.cuda.synchronize()
+        rows = np.sort(gen.choice(out, 64, replace=False))
+        rb = aa.weight_bytes(kind, inp, 1)
+        wr = np.ascontiguousarray(w.reshape(out, rb)[rows]).ravel()
+        want = oracle.qmatmul(kind, wr, inp, rows.size, X, nthreads=threads).astype(np.float64)
+        scale = np.abs(X.astype(np.float64)) @ np.abs(oracle.dequant(kind, wr, inp, rows.size)).astype(np.float64).T
+        got = yd.cpu().numpy()[:, rows].astype(np.float64)
+        err = float((np.abs(got - want) / np.maximum(scale, 1e-30)).max())
+        name = f"{aa.KIND_NAMES[kind]} {out}x{inp} B={B} ({small_batch_kernel(aa, kind, inp, out, B)})"
+        worst[name] = float(f"{err:.3e}")
+        if not err <= 1e-4:
+            print(f"bench.py: small batch {name} differs from the oracle: max err/sum|wx| {err:.3e} > 1e-4",
+                  file=sys.stderr, flush=True)
+            sys.exit(1)
+        del P, raw
+    return {"max_err_over_abs_dot": worst, "rtol": 1e-4, "rows_per_vector": 64}
+
+
+def moe_spot_check(torch, aa, gen, threads):
+    """Ties the moe_layer table's path to the oracle: the Qwen3-MoE layer shape
+    (router f32 [128][2048], 128 experts of gate/up Q4_K [768][2048] and down
+    Q6_K [2048][768], a gated shared expert, top-8) through the same device
+    entry points as the table (aspida_moe_route_dev, then
+    aspida_moe_experts_packed_dev) at T = 1, 8 and 32.  Per token: the GPU's
+    expert choice equals the oracle's rule applied to the GPU's logits
+    (llm_moe.adb:182-186), and the layer output equals the oracle's
+    LLM_MoE.Forward experts (llm_moe.adb:111-302) on that choice within 1e-4
+    of max |y|.  Exits if any is out."""
+    import numpy as np
+    import oracle
+    from aspida_amd import synth
+    dev = aa.DeviceOps()
+    dim, inter, n_exp, top_k = 2048, 768, 128, 8
+    gate = synth.weight_np(Q4_K, n_exp * inter, dim, gen)
+    up = synth.weight_np(Q4_K, n_exp * inter, dim, gen)
+    down = synth.weight_np(Q6_K, n_exp * dim, inter, gen)
+    shg, shu = synth.weight_np(Q4_K, inter, dim, gen), synth.weight_np(Q4_K, inter, dim, gen)
+    shd = synth.weight_np(Q6_K, dim, inter, gen)
+    router = (gen.standard_normal((n_exp, dim)) * 0.02).astype(np.float32)
+    sgi = (gen.standard_normal(dim) * 0.02).astype(np.float32)
+
+    def packed(kind, w, n, in_dim, out_dim):
+        src = torch.from_numpy(np.ascontiguousarray(w)).cuda()
+        dst = torch.empty(n * dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+        dev.pack_experts(kind, src.data_ptr(), src.numel() // n, in_dim, out_dim, n, dst.data_ptr())
+        return dst
+
+    P = {"gate": packed(Q4_K, gate, n_exp, dim, inter), "up": packed(Q4_K, up, n_exp, dim, inter),
+         "down": packed(Q6_K, down, n_exp, inter, dim), "shg": packed(Q4_K, shg, 1, dim, inter),
+         "shu": packed(Q4_K, shu, 1, dim, inter), "shd": packed(Q6_K, shd, 1, inter, dim)}
+    rd, sd = torch.from_numpy(router).cuda(), torch.from_numpy(sgi).cuda()
+    worst = {}
+    for T in (1, 8, 32):
+        X = (gen.standard_normal((T, dim))).astype(np.float32)
+        xd = torch.from_numpy(X).cuda()
+        f = dict(device="cuda", dtype=torch.float32)
+        logits, tw, y = torch.empty(T, n_exp, **f), torch.empty(T, top_k, **f), torch.empty(T, dim, **f)
+        idx = torch.empty(T, top_k, device="cuda", dtype=torch.int32)
+        work = torch.empty(dev.moe_packed_work_bytes(T, dim, inter, top_k), dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        dev.route(rd.data_ptr(), n_exp, dim, T, top_k, xd.data_ptr(), logits.data_ptr(), idx.data_ptr(),
+                  tw.data_ptr())
+        dev.moe_experts_packed(xd.data_ptr(), T, dim, top_k, inter, n_exp, idx.data_ptr(), tw.data_ptr(),
+                               P["gate"].data_ptr(), P["up"].data_ptr(), Q4_K, P["down"].data_ptr(), Q6_K,
+                               P["shg"].data_ptr(), P["shu"].data_ptr(), P["shd"].data_ptr(), sd.data_ptr(),
+                               work.data_ptr(), y.data_ptr())
+        torch.cuda.synchronize()
+        L, I, W, Y = logits.cpu().numpy(), idx.cpu().numpy(), tw.cpu().numpy(), y.cpu().numpy()
+        err = 0.0
+        for t in range(T):
+            ri, rw = oracle.route(L[t], top_k)
+            if not (np.array_equal(ri, I[t]) and np.allclose(rw, W[t], rtol=1e-5, atol=1e-7)):
+                print(f"bench.py: MoE T={T} token {t}: GPU routing {I[t]} differs from the oracle's rule on its "
+                      f"logits {ri}", file=sys.stderr, flush=True)
+                sys.exit(1)
+            want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, I[t], W[t], (gate, Q4_K), (up, Q4_K),
+                                      (down, Q6_K), (shg, Q4_K), (shu, Q4_K), (shd, Q6_K), sgi, nthreads=threads)
+            err = max(err, float(np.abs(Y[t].astype(np.float64) - want).max() / max(np.abs(want).max(), 1e-30)))
+        worst[f"T={T}"] = float(f"{err:.3e}")
+        if not err <= 1e-4:
+            print(f"bench.py: MoE layer T={T} differs from the oracle: max err / max|y| {err:.3e} > 1e-4",
+                  file=sys.stderr, flush=True)
+            sys.exit(1)
+    return {"max_err_over_max_abs_y": worst, "rtol": 1e-4, "routing": "GPU choice == oracle rule on GPU logits"}
 
 
 def _cpu_model():
@@ -835,7 +950,7 @@ def main():
         print(json.dumps({"decode_70b": decode_70b(torch, aa, synth, args.seed, stream, args.mv_engine, args.steps,
                                                    args.warmup)}), flush=True)
         return
-    if args.only:
+    if args.only and args.only != "resident":
         if args.copy_probe_mib:
             copy_probe(torch, args.copy_probe_mib)
         if args.only == "abi":
@@ -863,15 +978,19 @@ def main():
     tok_s = args.steps / wall
     print(f"# decode (per-matrix launches): {args.steps} tokens in {wall * 1e3:.1f} ms wall "
           f"({gpu_s * 1e3:.1f} ms events) = {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
-    # The same token as one resident-chain launch (aspida_kq_chain_*), reported beside it.
-    chain = dec.build_chain()
-    cwall, cgpu = timed(lambda sp: chain.run(sp), args.steps, args.warmup)
-    chain_ok = chain.check()
-    chain_info = {"tok_s": round(args.steps / cwall, 2), "ms_per_step": round(cwall * 1e3 / args.steps, 4),
-                  "gpu_event_ms_per_step": round(cgpu * 1e3 / args.steps, 4), "workgroups": chain.workgroups(),
-                  "waits_completed": bool(chain_ok)}
-    print(f"# decode (resident chain): {args.steps / cwall:.1f} tok/s", file=sys.stderr, flush=True)
-    chain.close()
+    if args.only == "resident":
+        # Experiment, not the headline: the same token as one persistent
+        # resident-chain launch (aspida_kq_chain_*), measured slower than the
+        # per-matrix launches.
+        chain = dec.build_chain()
+        cwall, cgpu = timed(lambda sp: chain.run(sp), args.steps, args.warmup)
+        chain_info = {"experiment": "persistent matvec chain (aspida_kq_chain_*)", "decode_tok_s": round(tok_s, 2),
+                      "tok_s": round(args.steps / cwall, 2), "ms_per_step": round(cwall * 1e3 / args.steps, 4),
+                      "gpu_event_ms_per_step": round(cgpu * 1e3 / args.steps, 4), "workgroups": chain.workgroups(),
+                      "waits_completed": bool(chain.check())}
+        chain.close()
+        print(json.dumps({"resident_chain": chain_info}), flush=True)
+        return
 
     # Dominant kernel: per kernel, its launches of one step in a graph of their own, timed with events.
     groups = kernel_events(torch, dec, stream)
@@ -932,7 +1051,6 @@ def main():
         "cpu_baseline": cpu,
         "abi_path": abi,
         "kernels": groups,
-        "resident_chain": chain_info,
         "kquant_matvec": table,
         "small_batch": small,
         "moe_layer": moe,

@@ -44,6 +44,39 @@ def test_matmul_config_batches(kind, batch, gpu):
                         what=f"{aa.KIND_NAMES[kind]} B={batch}")
 
 
+# BASELINE config 2 at its exact shapes: Q4_K and Q6_K weights of 4096 x 4096
+# and 14336 x 4096 times B = 2 ... 64 activation vectors, on the library's
+# default kernel pick (the same entry point and plans as bench.py's
+# small_batch table).  The whole product runs on the GPU; 96 of its rows
+# (the first and last 32 and 32 spread between) are checked against the
+# oracle's QMatVec per vector.
+CONFIG2_ROWS = 32
+
+
+def _sample_rows(out_dim, gen):
+    mid = np.sort(gen.choice(np.arange(CONFIG2_ROWS, out_dim - CONFIG2_ROWS), CONFIG2_ROWS, replace=False))
+    return np.concatenate([np.arange(CONFIG2_ROWS), mid, np.arange(out_dim - CONFIG2_ROWS, out_dim)])
+
+
+@pytest.mark.parametrize("batch", [2, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096)], ids=["4096x4096", "14336x4096"])
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+def test_config2_exact_shapes_default_pick(kind, shape, batch):
+    out_dim, in_dim = shape
+    gen = synth.rng(1200 + batch + out_dim // 1024 + 7 * kind)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    Y = _packed_matmul(kind, w, X, in_dim, out_dim)
+    rows = _sample_rows(out_dim, gen)
+    rb = aa.weight_bytes(kind, in_dim, 1)
+    wr = np.ascontiguousarray(w.reshape(out_dim, rb)[rows]).ravel()
+    want = oracle.qmatmul(kind, wr, in_dim, rows.size, X, nthreads=ncpu())
+    scale = _batched_scale(kind, wr, in_dim, rows.size, X)
+    assert np.all(np.isfinite(Y))
+    assert_close_scaled(Y[:, rows].ravel(), want.ravel(), scale.ravel(),
+                        what=f"config 2 {aa.KIND_NAMES[kind]} {out_dim}x{in_dim} B={batch}")
+
+
 # Shapes whose launches pad the batch to fewer vectors than the whole batch
 # (Q6_K in steps of 32, a tail of 1 or 16): the workspace must hold each
 # launch's finer column split (Qwen2-1.5B down, Qwen2-7B o).
