@@ -375,7 +375,8 @@ class DeviceOps:
         self._ok(self.lib.aspida_kq_set_mfma_rows(mode), "aspida_kq_set_mfma_rows")
 
     def set_mm_engine(self, engine):
-        """Batches > 1: 0 built-in choice, 1 VALU, 2 64-vector MFMA, 3 16-vector MFMA."""
+        """Batches > 1: 0 built-in choice, 1 VALU, 2 64-vector MFMA, 3 16-vector MFMA,
+        4 one-pass MFMA, 5 batch-1 MFMA on up to 4 vectors, 6 wave-per-column MFMA."""
         self._ok(self.lib.aspida_kq_set_mm_engine(engine), "aspida_kq_set_mm_engine")
 
 

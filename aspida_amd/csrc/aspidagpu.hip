@@ -252,6 +252,7 @@ size_t mm_work_bytes(int in_dim, int out_dim, int batch) {
     n = std::max(n, kq::mfma_workspace_bytes(in_dim, out_dim, bp));
     if (bp >= batch) break;
   }
+  if (in_dim % 1024 == 0) n = std::max(n, kq::mmw_workspace_bytes(in_dim, out_dim, std::min(batch, 64)));
   return n;
 }
 
@@ -275,8 +276,8 @@ struct MvWorkspace {
 // Y[batch][out] = X W^T over packed W on `st`.  Batch 1 is the matvec.
 // Otherwise, by g_mm_engine: 0 picks, 1 forces the multi-vector VALU kernel,
 // 2 the 64-vector and 3 the 16-vector MFMA kernel, 4 the one-pass kernel
-// (kq_mmv.hip) and 5 the batch-1 kernel for up to 4 vectors per launch,
-// where the kind has one.
+// (kq_mmv.hip), 5 the batch-1 kernel for up to 4 vectors per launch and 6
+// the wave-per-column kernel (kq_mmw.hip), where the kind has one.
 // The pick for Q4_K and Q6_K (measured on MI355X at 4096x4096 and
 // 14336x4096, `small_batch` of bench.py):
 //   up to 4 vectors: the batch-1 kernel on 4 vectors where its batch-1
@@ -324,6 +325,7 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   // vectors in one launch, 82 us per 32).
   if (eng == 4 && kq::mmv_kind(kind)) return {3, 64};
   if (eng == 5 && kq::matvec_nv_takes(kind, in_dim, out_dim)) return {4, 4};
+  if (eng == 6 && kq::mmw_takes(kind, in_dim)) return {5, 64};
   if (eng == 0 && kq::mmv_kind(kind) && kq::matvec_nv_takes(kind, in_dim, out_dim)) {
     // Very tall matrices (output heads): the 16-vector kernel, whose
     // activation pre-pass is amortised over many rows.
@@ -346,6 +348,7 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
 size_t mm_launch_need(int kind, int in_dim, int out_dim, int batch) {
   if (batch <= 1) return 0;
   const MmRoute r = mm_route(kind, in_dim, out_dim, batch);
+  if (r.family == 5) return kq::mmw_workspace_bytes(in_dim, out_dim, std::min(batch, r.step));
   if (r.family == 0 || r.family >= 3) return 0;
   if (r.family == 1) return kq::mm16_workspace_bytes(in_dim, out_dim);
   size_t n = kq::mfma_workspace_bytes(in_dim, out_dim, std::min(batch, r.step));
@@ -367,6 +370,8 @@ hipError_t matmul_packed(int kind, const void* P, int in_dim, int out_dim, int b
       e = kq::launch_matvec_mfma_nv(kind, P, in_dim, out_dim, nb, xb, yb, st);
     else if (r.family == 3)
       e = kq::launch_matmul_mmv(kind, P, in_dim, out_dim, nb, xb, yb, st);
+    else if (r.family == 5)
+      e = kq::launch_matmul_mmw(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st);
     else if (r.family == 1)
       e = kq::launch_matmul_mm16(kind, P, in_dim, out_dim, nb, xb, yb, ws.mm.p, ws.count.p, st, batch <= r.step);
     else if (r.family == 2)
@@ -1185,7 +1190,7 @@ extern "C" int aspida_kq_set_mv_engine(int engine) {
 }
 
 extern "C" int aspida_kq_set_mm_engine(int engine) {
-  if (engine < 0 || engine > 5) return -EINVAL;
+  if (engine < 0 || engine > 6) return -EINVAL;
   g_mm_engine = engine;
   return 0;
 }

@@ -151,4 +151,21 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 }
 #endif
 
+// The bits of the largest |x| over the wave's float4s, in every lane.
+// Non-negative floats order as their bit patterns do, so the reduction is an
+// unsigned max on DPP-fused instructions; a NaN sorts above every finite
+// value (its column then takes S = 1; its outputs are NaN either way).
+__device__ __forceinline__ uint32_t wave_max_abs_bits(float4 v) {
+  uint32_t m = max(max(__builtin_bit_cast(uint32_t, v.x) & 0x7FFFFFFFu, __builtin_bit_cast(uint32_t, v.y) & 0x7FFFFFFFu),
+                   max(__builtin_bit_cast(uint32_t, v.z) & 0x7FFFFFFFu, __builtin_bit_cast(uint32_t, v.w) & 0x7FFFFFFFu));
+  auto step = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x111, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x112, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x114, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x118, 0xF, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x142, 0xA, 0xF, true));
+  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x143, 0xC, 0xF, true));
+  return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
+}
+
 }  // namespace kq

@@ -106,6 +106,17 @@ bool mmv_kind(int kind);
 int mmv_step(int kind, int in_dim, int out_dim);
 hipError_t launch_matmul_mmv(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
                              hipStream_t s);
+// Small batches of up to 64 vectors over packed Q4_K / Q6_K, one wave per
+// (64-row tile, super-block column) (kq_mmw.hip): the activation split of
+// kq_xsplit, then four columns per workgroup summed in LDS and mmw_ks column
+// groups per tile summed through partials.  `work` holds
+// mmw_workspace_bytes; `count` one counter per tile, zero before first use
+// and left zero.  in_dim must be a multiple of 1024.
+bool mmw_takes(int kind, int in_dim);
+int mmw_ks(int in_dim, int out_dim);
+size_t mmw_workspace_bytes(int in_dim, int out_dim, int batch);
+hipError_t launch_matmul_mmw(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,
+                             void* work, unsigned* count, hipStream_t s);
 bool mm16_kind(int kind);
 size_t mm16_workspace_bytes(int in_dim, int out_dim);
 hipError_t launch_matmul_mm16(int kind, const void* P, int in_dim, int out_dim, int batch, const float* X, float* Y,

@@ -79,6 +79,10 @@ __device__ __forceinline__ float mmv_rows_sum(float v) {
 
 // Sub-block sums of x S (|.| <= 32 2^14) times this fit f16.
 constexpr float MMV_XSUM = 1.f / 64.f;
+// Largest scale exponent: S 2^11 = 2^(se + 11) must stay a finite f32 (a
+// column whose largest |x| is below 2^-102 takes S = 2^116, its values then
+// at most 2^10 after scaling, still far inside f16's range).
+constexpr int MMV_SE_MAX = 116;
 
 template <> struct MmvX<Q4_K> {
   uint4 ah[8], al[8];
@@ -103,7 +107,7 @@ template <> struct MmvX<Q4_K> {
     int e = 0;
     const bool scaled = mx > 0.f && __builtin_isfinite(mx);
     if (scaled) (void)frexpf(mx, &e);
-    const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
+    const int se = scaled ? std::min(std::max(14 - e, -120), MMV_SE_MAX) : 0;
     const float S = ldexpf(1.f, se), S11 = ldexpf(1.f, se + 11);
     float su[8];
 #pragma unroll
@@ -149,7 +153,7 @@ template <> struct MmvX<Q6_K> {
     int e = 0;
     const bool scaled = mx > 0.f && __builtin_isfinite(mx);
     if (scaled) (void)frexpf(mx, &e);
-    const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
+    const int se = scaled ? std::min(std::max(14 - e, -120), MMV_SE_MAX) : 0;
     const float S = ldexpf(1.f, se), S11 = ldexpf(1.f, se + 11);
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -202,7 +206,7 @@ __device__ __forceinline__ void mmv_build_staged(MmvX<KIND>& A, MmvStage<GV>& st
   int e = 0;
   const bool scaled = mx > 0.f && __builtin_isfinite(mx);
   if (scaled) (void)frexpf(mx, &e);
-  const int se = scaled ? std::min(std::max(14 - e, -120), 120) : 0;
+  const int se = scaled ? std::min(std::max(14 - e, -120), MMV_SE_MAX) : 0;
   const float S = ldexpf(1.f, se), S11 = ldexpf(1.f, se + 11);
   float su = 0.f;
 #pragma unroll

@@ -76,23 +76,6 @@ __device__ __forceinline__ MvLane mv_lane(uint4 (&img)[8][IL], int lane) {
   return L;
 }
 
-// The bits of the largest |x| over the wave's float4s, in every lane.
-// Non-negative floats order as their bit patterns do, so the reduction is an
-// unsigned max on DPP-fused instructions; a NaN sorts above every finite
-// value (its column then takes S = 1; its outputs are NaN either way).
-__device__ __forceinline__ uint32_t wave_max_abs_bits(float4 v) {
-  uint32_t m = max(max(__builtin_bit_cast(uint32_t, v.x) & 0x7FFFFFFFu, __builtin_bit_cast(uint32_t, v.y) & 0x7FFFFFFFu),
-                   max(__builtin_bit_cast(uint32_t, v.z) & 0x7FFFFFFFu, __builtin_bit_cast(uint32_t, v.w) & 0x7FFFFFFFu));
-  auto step = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x111, 0xF, 0xF, true));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x112, 0xF, 0xF, true));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x114, 0xF, 0xF, true));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x118, 0xF, 0xF, true));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x142, 0xA, 0xF, true));
-  m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x143, 0xC, 0xF, true));
-  return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
-}
-
 // Builds the column's A image and sub-block sums of x S from the lane's
 // float4 of x; returns 1/S.  S = 2^se puts the column's largest |x| just below
 // 2^14: se = 14 - e for max |x| = f 2^e, f in [0.5, 1), i.e. 140 minus its

@@ -419,8 +419,10 @@ int aspida_kq_set_mv_engine(int engine);
  * kernel for Q4_K; other kinds on the vector kernel); 1 = the vector kernel; 2 = the 64-vector and 3 = the
  * 16-vector matrix-core kernel; 4 = the one-pass matrix-core kernel (up to
  * 64 vectors per weight pass); 5 = the batch-1 matrix-core kernel on up to 4
- * vectors per launch; for the kinds that have one (others stay on the
- * vector kernel).
+ * vectors per launch; 6 = the wave-per-column matrix-core kernel (Q4_K and
+ * Q6_K with in_dim a multiple of 1024: one wave per 64-row tile and
+ * 256-element column, activations split in a pre-pass); for the kinds that
+ * have one (others stay on the vector kernel).
  * Per calling thread; for comparison and tests.  No reference counterpart.
  * Returns 0, or -EINVAL for another value. */
 int aspida_kq_set_mm_engine(int engine);

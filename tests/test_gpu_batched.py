@@ -216,10 +216,11 @@ MM_ENGINE_CASES = [(2, 130, 768), (5, 64, 4096), (16, 1000, 4096), (17, 67, 2304
 # Engine 4 is the one-pass kernel (kq_mmv.hip): 64-row tiles from 12352 rows
 # (193 tiles), 16-row blocks below; up to 64 vectors in one launch, up to 4
 # converted through LDS.  Engine 5
-# runs up to 4 vectors per launch on the batch-1 16-row kernels.  Engine 0 is
-# the library's pick (Q6_K on 64-row tiles above 32 vectors: launches of 32
-# on the one-pass kernel).
-@pytest.mark.parametrize("engine", [0, 1, 2, 3, 4, 5])
+# runs up to 4 vectors per launch on the batch-1 16-row kernels.  Engine 6 is
+# the wave-per-column kernel (kq_mmw.hip) where in_dim is a multiple of 1024
+# (columns split over waves, workgroups and, for 12352 rows at 4096, column
+# groups), the vector kernel elsewhere.  Engine 0 is the library's pick.
+@pytest.mark.parametrize("engine", [0, 1, 2, 3, 4, 5, 6])
 @pytest.mark.parametrize("case", MM_ENGINE_CASES, ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
 @pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
 def test_mm_engines_match_oracle(kind, case, engine):
@@ -236,6 +237,30 @@ def test_mm_engines_match_oracle(kind, case, engine):
     want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
     assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
                         what=f"engine {engine} B={batch} {out_dim}x{in_dim}")
+
+
+# Columns whose largest |x| is below 2^-102 take the largest activation scale
+# (2^116, so that the lo plane's factor S 2^11 stays finite): tiny and mixed
+# magnitudes through the matrix-core small-batch engines (4 the one-pass
+# kernel, 6 the wave-per-column kernel, 0 the pick), one 64-row tile
+# (columns split over workgroups) and several.
+@pytest.mark.parametrize("engine", [0, 4, 6])
+@pytest.mark.parametrize("case", [(16, 64, 4096), (40, 4096, 4096), (64, 12352, 512)],
+                         ids=lambda c: f"B{c[0]}_{c[1]}x{c[2]}")
+@pytest.mark.parametrize("kind", [aa.Q4_K, aa.Q6_K], ids=["Q4_K", "Q6_K"])
+def test_mm_engines_tiny_activations(kind, case, engine):
+    batch, out_dim, in_dim = case
+    gen = synth.rng(1300 + batch + out_dim)
+    w = synth.weight_np(kind, out_dim, in_dim, gen)
+    X = synth.activations_np(batch * in_dim, gen).reshape(batch, in_dim)
+    X[0] *= np.float32(1e-33)                       # every column of vector 0 below 2^-102
+    X[1, :256] *= np.float32(1e-33)                 # one column of vector 1
+    X[2, 256:512] *= np.float32(3e4)                 # a large column
+    Y = _engine_matmul(engine, kind, w, X, in_dim, out_dim)
+    want = oracle.qmatmul(kind, w, in_dim, out_dim, X, nthreads=ncpu())
+    assert np.all(np.isfinite(Y))
+    assert_close_scaled(Y.ravel(), want.ravel(), _batched_scale(kind, w, in_dim, out_dim, X).ravel(),
+                        what=f"engine {engine} tiny B={batch} {out_dim}x{in_dim}")
 
 
 def _engine_matmul(engine, kind, w, X, in_dim, out_dim):
