@@ -168,4 +168,5 @@ __device__ __forceinline__ uint32_t wave_max_abs_bits(float4 v) {
   return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
 }
 
+
 }  // namespace kq

@@ -8,6 +8,7 @@
 // launch with its activations in registers, and overlaps the next row
 // block's loads with the current block's arithmetic.
 #include "kq_blocks.h"
+#include "kq_elem.h"
 #include "kq_kernels.h"
 
 namespace kq {
@@ -204,68 +205,7 @@ __global__ __launch_bounds__(256) void dense_mv(const float* __restrict__ W, int
   if (lane == 0) y[row] = acc;
 }
 
-// ---- bit-exact dequantization (test export).  Element P of a super-block is
-// computed with the CPU decoder's own operation order, one rounding, so the
-// f32 bits equal Decode_Q*K_Block's (llm_dequant.adb:122-554).
-template <int KIND>
-__device__ float dequant_elem(const uint8_t* b, int P);
-
-__device__ __forceinline__ void get_sm(const uint8_t* sc, int j, int& s, int& m) {
-  if (j < 4) { s = sc[j] & 63; m = sc[j + 4] & 63; }
-  else { s = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4); m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4); }
-}
-
-template <> __device__ float dequant_elem<Q4_K>(const uint8_t* b, int P) {
-  const int g = P / 64, hi = (P % 64) / 32, l = P % 32;
-  int s, m;
-  get_sm(b + 4, 2 * g + hi, s, m);
-  const float d = f16_ada(ld2(b)), dmin = f16_ada(ld2(b + 2));
-  const uint32_t q = b[16 + 32 * g + l];
-  const float D = d * (float)s, M = dmin * (float)m;
-  return __fsub_rn(__fmul_rn(D, (float)(hi ? (q >> 4) : (q & 15))), M);
-}
-template <> __device__ float dequant_elem<Q5_K>(const uint8_t* b, int P) {
-  const int g = P / 64, hi = (P % 64) / 32, l = P % 32;
-  int s, m;
-  get_sm(b + 4, 2 * g + hi, s, m);
-  const float d = f16_ada(ld2(b)), dmin = f16_ada(ld2(b + 2));
-  const uint32_t q = b[48 + 32 * g + l], h = b[16 + l];
-  const uint32_t v = (hi ? (q >> 4) : (q & 15)) + (((h >> (2 * g + hi)) & 1u) << 4);
-  return __fsub_rn(__fmul_rn(d * (float)s, (float)v), dmin * (float)m);
-}
-template <> __device__ float dequant_elem<Q6_K>(const uint8_t* b, int P) {
-  const int h = P / 128, k = (P % 128) / 32, l = P % 32;
-  const uint32_t ql = b[64 * h + l + (k & 1) * 32], qh = b[128 + 32 * h + l];
-  const uint32_t lo = (k & 2) ? (ql >> 4) : (ql & 15);
-  const int q = (int)(lo | (((qh >> (2 * k)) & 3u) << 4)) - 32;
-  const int sc = (int8_t)b[192 + 8 * h + l / 16 + 2 * k];
-  const float d = f16_ada(ld2(b + 208));
-  return __fmul_rn(d * (float)sc, (float)q);
-}
-template <> __device__ float dequant_elem<Q3_K>(const uint8_t* b, int P) {
-  const int nh = P / 128, j = (P % 128) / 32, g = (P % 32) / 16, l = P % 16;
-  const int low2 = (b[32 + 32 * nh + 16 * g + l] >> (2 * j)) & 3;
-  const int hbit = (b[16 * g + l] >> (4 * nh + j)) & 1;
-  const int is = 8 * nh + 2 * j + g;
-  // 6-bit scale is: low nibble from byte is%8 of scales[0..7] (shifted by 4
-  // for is >= 8), high two bits from scales[8 + is%4] at bit 2*(is/4).
-  const uint32_t lo4 = (b[96 + (is % 8)] >> (4 * (is / 8))) & 15u;
-  const uint32_t hi2 = (b[104 + (is % 4)] >> (2 * (is / 4))) & 3u;
-  const int sc = (int)(lo4 | (hi2 << 4)) - 32;
-  const float d = f16_ada(ld2(b + 108));
-  return __fmul_rn(__fmul_rn(d, (float)sc), (float)(low2 + 4 * hbit - 4));
-}
-template <> __device__ float dequant_elem<Q2_K>(const uint8_t* b, int P) {
-  const int nh = P / 128, j = (P % 128) / 32, g = (P % 32) / 16, l = P % 16;
-  const uint32_t sc = b[8 * nh + 2 * j + g];
-  const float q = (float)((b[16 + 32 * nh + 16 * g + l] >> (2 * j)) & 3);
-  const float d = f16_ada(ld2(b + 80)), dmin = f16_ada(ld2(b + 82));
-  return __fsub_rn(__fmul_rn(d * (float)(sc & 15), q), dmin * (float)(sc >> 4));
-}
-template <> __device__ float dequant_elem<Q8_0>(const uint8_t* b, int P) {
-  const uint8_t* blk = b + 34 * (P / 32);
-  return __fmul_rn(f16_ada(ld2(blk)), (float)(int8_t)blk[2 + P % 32]);
-}
+// ---- bit-exact dequantization (test export): dequant_elem, kq_elem.h.
 
 template <int KIND>
 __global__ void kq_dequant(const uint8_t* __restrict__ W, size_t row_bytes, int nsb, int out_rows,
@@ -275,7 +215,7 @@ __global__ void kq_dequant(const uint8_t* __restrict__ W, size_t row_bytes, int 
   if (i >= per_row * (size_t)out_rows) return;
   const size_t o = i / per_row, e = i % per_row;
   const uint8_t* sb = W + o * row_bytes + (e / 256) * Block<KIND>::BYTES;
-  dst[i] = dequant_elem<KIND>(sb, (int)(e % 256));
+  dst[i] = dequant_elem<KIND>(RowMajorBytes{sb}, (int)(e % 256));
 }
 
 // ---- launchers --------------------------------------------------------------

@@ -230,14 +230,15 @@ __global__ __launch_bounds__(128 * NWG) void moe_gate_up1(MoeGroupedArgs a, int 
 // xv are loaded: the arithmetic of mv_mfma_rows<KIND, MV_ONE, 1> from the
 // image build on (the same results).
 template <int KIND>
-__device__ __forceinline__ float moe1_unit(const MvCol<KIND, 1>& c, float4 xv, MvShared16& sh, int lane) {
+__device__ __forceinline__ float moe1_unit(const MvCol<KIND, 1>& c, float4 xv, MvShared16& sh, int lane,
+                                           const uint8_t* grp, const float* xs, int rb0) {
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     if (lane < 17) sh.img[j][lane] = make_uint4(0u, 0u, 0u, 0u);
   const MvLane L = mv_lane<KIND>(sh.img, lane);
   float acc[1] = {0.f};
-  mv_column<1, 17>(c, xv, L, sh.img, sh.xsum, (MvHdr<KIND>*)nullptr, lane, acc);
+  mv_column<KIND, 1, 17>(c, xv, L, sh.img, sh.xsum, (MvHdr<KIND>*)nullptr, lane, acc, grp, xs, rb0);
   float* red = reinterpret_cast<float*>(&sh.img[0][0]);
   __builtin_amdgcn_wave_barrier();
   red[lane] = acc[0];
@@ -269,10 +270,12 @@ __global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
     w0.load(M0 + ((size_t)(b >> 2) * nsb + c0) * GB, lane, b & 3);
     const float4 x1 = ld_f4(a.h + (size_t)k1 * a.I + (size_t)c1 * 256 + 4 * lane);
     w1.load(M1 + ((size_t)(b >> 2) * nsb + c1) * GB, lane, b & 3);
-    const float r0 = moe1_unit<KIND>(w0, x0, sh[w], lane);
+    const float r0 = moe1_unit<KIND>(w0, x0, sh[w], lane, M0 + ((size_t)(b >> 2) * nsb + c0) * GB,
+                                     a.h + (size_t)k0 * a.I + (size_t)c0 * 256, b & 3);
     if (lane < 16) part[u][lane] = r0;
     if (v != u) {
-      const float r1 = moe1_unit<KIND>(w1, x1, sh[w], lane);
+      const float r1 = moe1_unit<KIND>(w1, x1, sh[w], lane, M1 + ((size_t)(b >> 2) * nsb + c1) * GB,
+                                       a.h + (size_t)k1 * a.I + (size_t)c1 * 256, b & 3);
       if (lane < 16) part[v][lane] = r1;
     }
   }

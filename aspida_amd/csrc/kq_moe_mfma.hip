@@ -112,7 +112,7 @@ __device__ __forceinline__ void mr_build(MrImg (&img)[MR_J][MR_GC], const float4
       const int jj = i / gc, c = i - jj * gc;
       MrImg& m = img[jj][c];
       const MvLane L = mv_lane<KIND, 17>(m.q, lane);
-      const float invS = build_image<KIND>(xv[k], L, m.xsum);
+      const float invS = build_image<KIND>(xv[k], L, m.xsum, wave_max_abs_bits(xv[k]));
       if (lane == 0) m.invS = invS;
     }
   }

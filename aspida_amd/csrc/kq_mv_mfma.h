@@ -6,6 +6,7 @@
 #pragma once
 #include <algorithm>
 
+#include "kq_elem.h"
 #include "kq_packed.h"
 
 namespace kq {
@@ -82,8 +83,8 @@ __device__ __forceinline__ MvLane mv_lane(uint4 (&img)[8][IL], int lane) {
 // biased exponent, at most 120 (0 for an all-zero column or a non-finite
 // maximum).  The exponent arithmetic is wave-uniform (scalar instructions).
 template <int KIND>
-__device__ __forceinline__ float build_image(float4 xv, const MvLane& L, float* xsum) {
-  const uint32_t mx = wave_max_abs_bits(xv);
+__device__ __forceinline__ float build_image(float4 xv, const MvLane& L, float* xsum,
+                                             uint32_t mx /* wave_max_abs_bits(xv) */) {
   const int se = (mx == 0u || mx >= 0x7F800000u) ? 0 : std::min(140 - (int)(mx >> 23), 120);
   const float S = __builtin_bit_cast(float, (uint32_t)(se + 127) << 23);
   const float sl = S * L.odd;
@@ -291,14 +292,6 @@ __device__ __forceinline__ void mv_dot(const MvCol<Q4_K, RB>& c, const uint4 (&i
   }
 }
 
-template <int RB, int IL = (RB == 4 ? 64 : 17)>
-__device__ __forceinline__ void mv_column(const MvCol<Q4_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q4_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q4_K>(xv, L, xsum);
-  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
-}
 
 template <int RB, int IL>
 __device__ __forceinline__ void mv_dot(const MvCol<Q6_K, RB>& c, const uint4 (&img)[8][IL], const float* xsum,
@@ -364,14 +357,6 @@ __device__ __forceinline__ void mv_dot(const MvCol<Q6_K, RB>& c, const uint4 (&i
   }
 }
 
-template <int RB, int IL = (RB == 4 ? 64 : 17)>
-__device__ __forceinline__ void mv_column(const MvCol<Q6_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q6_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q6_K>(xv, L, xsum);
-  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
-}
 
 // Q5_K (Decode_Q5K_Block, llm_dequant.adb:426-498): Q4_K's columns with a
 // fifth code bit, code = nibble + 16 hbit.  The nibbles take Q4_K's MFMAs; the
@@ -429,14 +414,6 @@ __device__ __forceinline__ void mv_dot(const MvCol<Q5_K, RB>& c, const uint4 (&i
   }
 }
 
-template <int RB, int IL = (RB == 4 ? 64 : 17)>
-__device__ __forceinline__ void mv_column(const MvCol<Q5_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q5_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q5_K>(xv, L, xsum);
-  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
-}
 
 // Q2_K: element 128 nh + 32 k + 16 g + l is field k of qs byte
 // 32 nh + 16 g + l with scale/min byte 8 nh + 2 k + g (Decode_Q2K_Block,
@@ -504,14 +481,6 @@ __device__ __forceinline__ void mv_dot(const MvCol<Q2_K, RB>& c, const uint4 (&i
   }
 }
 
-template <int RB, int IL = (RB == 4 ? 64 : 17)>
-__device__ __forceinline__ void mv_column(const MvCol<Q2_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q2_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
-  __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q2_K>(xv, L, xsum);
-  mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
-}
 
 // Q3_K (Decode_Q3K_Block, llm_dequant.adb:207-268): Q2_K's element layout
 // with a high bit, code = low2 + 4 hbit, w = d (sc - 32) (code - 4).  Since
@@ -582,13 +551,82 @@ __device__ __forceinline__ void mv_dot(const MvCol<Q3_K, RB>& c, const uint4 (&i
   }
 }
 
-template <int RB, int IL = (RB == 4 ? 64 : 17)>
-__device__ __forceinline__ void mv_column(const MvCol<Q3_K, RB>& c, float4 xv, const MvLane& L,
-                                          uint4 (&img)[8][IL], float* xsum, MvHdr<Q3_K>* hdr, int lane,
-                                          float (&acc)[RB]) {
+
+// One super-block column (weights c, activations xv of the column at xs,
+// group grp of the packed layout, row block rb0 when RB = 1): the A image of
+// the wave's 256 activations, then the kind's dot.
+//
+// Dominant activations.  The matrix cores do not round each addition of a
+// product sum: a product much smaller than the largest one in the same sum
+// keeps fewer bits (about 2^-18 of the largest).  Where a dominant
+// activation's weight cancels against a min or code-offset term, that loss
+// would stay behind against a small sum |w x| (with one 10^4x activation:
+// up to 4.3e-4 of it for Q2_K, 2.6e-4 for Q6_K, 2.4e-4 for Q3_K; Q4_K and
+// Q5_K stay below 1e-4).  For Q2_K, Q3_K and Q6_K, a column where at most 16
+// activations are within 16x of its largest |x| has those activations
+// zeroed in the image and its sub-block sums, and each lane adds w x for them
+// in f32, w its row's dequantized weight read from the packed group
+// (dequant_elem, bit-exact); row r's terms go to lane (r % 16, 0)'s
+// accumulator of block r / 16.  Other columns pay only the test: four
+// compares against max |x| / 16 and a count of the ballots (an ordinary
+// column has most of its 256 activations within 16x of its largest).
+template <int KIND> constexpr bool MV_EXACT_DOMINANT = KIND == Q2_K || KIND == Q3_K || KIND == Q6_K;
+
+template <int KIND, int RB, int IL = (RB == 4 ? 64 : 17)>
+__device__ __forceinline__ void mv_column(const MvCol<KIND, RB>& c, float4 xv, const MvLane& L,
+                                          uint4 (&img)[8][IL], float* xsum, MvHdr<KIND>* hdr, int lane,
+                                          float (&acc)[RB], const uint8_t* grp, const float* xs, int rb0) {
   __builtin_amdgcn_wave_barrier();
-  const float invS = build_image<Q3_K>(xv, L, xsum);
+  uint32_t mx = wave_max_abs_bits(xv);
+  uint64_t bits[4] = {0u, 0u, 0u, 0u};
+  bool exact = false;
+  if constexpr (MV_EXACT_DOMINANT<KIND>) {
+    // A non-finite maximum makes thr infinite or NaN: no dominant set is
+    // taken out unless some |x| is infinite (their products are not finite
+    // either way).
+    const float thr = __builtin_bit_cast(float, mx) * 0.0625f;
+    const bool dx = __builtin_fabsf(xv.x) >= thr, dy = __builtin_fabsf(xv.y) >= thr;
+    const bool dz = __builtin_fabsf(xv.z) >= thr, dw = __builtin_fabsf(xv.w) >= thr;
+    bits[0] = __ballot(dx);
+    bits[1] = __ballot(dy);
+    bits[2] = __ballot(dz);
+    bits[3] = __ballot(dw);
+    const int n = __builtin_popcountll(bits[0]) + __builtin_popcountll(bits[1]) + __builtin_popcountll(bits[2]) +
+                  __builtin_popcountll(bits[3]);
+    exact = __builtin_expect(n > 0 && n <= 16, 0);
+    if (exact) {
+      xv.x = dx ? 0.f : xv.x;
+      xv.y = dy ? 0.f : xv.y;
+      xv.z = dz ? 0.f : xv.z;
+      xv.w = dw ? 0.f : xv.w;
+      mx = wave_max_abs_bits(xv);
+    }
+  }
+  const float invS = build_image<KIND>(xv, L, xsum, mx);
   mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
+  if (MV_EXACT_DOMINANT<KIND> && exact) {  // after the dot, when its registers are free
+    const PackedBytes<KIND> wr(grp, RB == 4 ? lane : 16 * rb0 + (lane & 15));
+    float t = 0.f;
+    // One dominant element at a time (bit i of component cpt's ballot is
+    // element 4 i + cpt): the loop stays rolled, so only one element's
+    // decode is live.
+    uint64_t m = bits[0];
+    int cpt = 0;
+#pragma nounroll
+    while (true) {
+      while (m == 0 && cpt < 3) m = bits[++cpt];
+      if (m == 0) break;
+      const int e = 4 * (int)__builtin_ctzll(m) + cpt;
+      m &= m - 1;
+      t = __builtin_fmaf(dequant_elem<KIND>(wr, e), xs[e], t);
+    }
+    const bool g0 = (lane >> 4) == 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float u = RB == 4 ? __shfl(t, 16 * rb + (lane & 15), 64) : t;
+      if (g0) acc[rb] += u;
+    }
+  }
 }
 
 // The LDS one wave uses: its A image, sub-block sums and row headers.
@@ -626,7 +664,8 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
                                               float* xsum, MvHdr<KIND>* hdr, int lane, int rb0 = 0) {
   constexpr int GB = 64 * Block<KIND>::BYTES;
   const uint8_t* gp = P + ((size_t)tile * nsb + sb0) * GB;
-  const float* xp = x + (size_t)sb0 * 256 + 4 * lane;
+  const float* xc = x + (size_t)sb0 * 256;  // the wave's first column (uniform)
+  const float* xp = xc + 4 * lane;
 
   // Each column's activations are requested before its weights: the loads
   // return in order, so the activation image can be built while the weights
@@ -644,7 +683,7 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.f;
   if (PIPE == MV_ONE) {
-    mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+    mv_column(c0, x0, L, img, xsum, hdr, lane, acc, gp, xc, rb0);
   } else if (PIPE == MV_SEQ) {  // columns one after another: one register set, more waves per CU
     for (int s = 0; s < spw; ++s) {
       if (s > 0) {
@@ -652,7 +691,7 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
         __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)s * 256, 16), 16);
         c0.load(gp + (size_t)s * GB, lane, rb0);
       }
-      mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+      mv_column(c0, x0, L, img, xsum, hdr, lane, acc, gp + (size_t)s * GB, xc + (size_t)s * 256, rb0);
     }
   } else {
     // Two register sets used in turn: the next column's loads are in flight
@@ -664,13 +703,14 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
       __builtin_memcpy(&x1, __builtin_assume_aligned(xp + (size_t)s1 * 256, 16), 16);
       c1.load(gp + (size_t)s1 * GB, lane, rb0);
       asm volatile("" ::: "memory");  // keep these loads issued here
-      mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
+      mv_column(c0, x0, L, img, xsum, hdr, lane, acc, gp + (size_t)s * GB, xc + (size_t)s * 256, rb0);
       if (s + 2 < spw) {
         __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)(s + 2) * 256, 16), 16);
         c0.load(gp + (size_t)(s + 2) * GB, lane, rb0);
         asm volatile("" ::: "memory");
       }
-      if (s + 1 < spw) mv_column(c1, x1, L, img, xsum, hdr, lane, acc);
+      if (s + 1 < spw)
+        mv_column(c1, x1, L, img, xsum, hdr, lane, acc, gp + (size_t)s1 * GB, xc + (size_t)s1 * 256, rb0);
     }
   }
 
@@ -729,7 +769,9 @@ __device__ __forceinline__ void mv_mfma_rows_nv(const uint8_t* __restrict__ P, i
       c0.load(gp + (size_t)s * GB, lane, rb0);
     }
 #pragma unroll
-    for (int v = 0; v < NV; ++v) mv_column(c0, xv[v], L, img, xsum, hdr, lane, acc[v]);
+    for (int v = 0; v < NV; ++v)
+      mv_column(c0, xv[v], L, img, xsum, hdr, lane, acc[v], gp + (size_t)s * GB,
+                x + (size_t)(v < nv ? v : nv - 1) * ldx + (size_t)(sb0 + s) * 256, rb0);
   }
   // Lane (n, g) holds rows 16 rb + n over its quarter: add the four quarters
   // (ascending g), vector by vector.

@@ -422,20 +422,57 @@ def test_engines_activation_range(kind, engine, dev):
                 dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
                 sync()
                 want = oracle.qmatvec(kind, w, in_dim, out_dim, x, nthreads=ncpu())
-                # Q2_K's 2-bit codes with mins: for an outlier element d sc q and dmin m nearly
-                # cancel, so the matrix cores' error relative to the large q x term weighs more
-                # against sum |w x| (measured 1.3e-4; the north-star bar is 1e-3).  Q3_K splits
-                # code - 4 into low2 - 4 (1 - hbit): a code-3 outlier is +3 x in one sum and -4 x
-                # in the other, each with the matrix cores' error of its own size (measured
-                # 1.2e-4 here, 2.4e-4 with one 1e4x element dominating a row).
-                wide = kind in (aa.Q2_K, aa.Q3_K)
-                rtol = (MFMA_RTOL * (3 if wide else 1) if engine == 0 and name in ("outliers", "mixed")
-                        else MV_RTOL)
+                # Outliers: the matrix cores keep about 2^-18 of a sum's largest product, and an
+                # outlier whose weight cancels against the min term leaves that behind.  Q2_K,
+                # Q3_K and Q6_K take a column's dominant activations exactly (measured <= 2.6e-5
+                # here); Q4_K and Q5_K keep them in the matrix-core sums (measured 7.3e-5 and
+                # 7.9e-5 on the 512-column rows, where one column weighs most).
+                rtol = MFMA_RTOL if engine == 0 and name in ("outliers", "mixed") else MV_RTOL
                 r = assert_close_scaled(dy.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x),
                                         rtol=rtol, what=f"engine {engine} {out_dim}x{in_dim} {name}")
                 print(f"  max err / sum|wx| = {r:.2e}", flush=True)
     finally:
         dev.set_mv_engine(0)
+
+
+@pytest.mark.parametrize("kind", [aa.Q6_K, aa.Q2_K, aa.Q3_K], ids=["Q6_K", "Q2_K", "Q3_K"])
+def test_dominant_activations_exact(kind, dev):
+    """Columns whose activations are dominated by a few (at most 16 within 16x
+    of the largest) take those activations out of the matrix-core sums: one
+    1e6x element, 16 elements at 1e4x (the largest set taken out), 17 at 1e4x
+    (left in: they carry most of sum |w x| themselves), and a column with
+    only three nonzero entries, on both workgroup shapes.  Held to 3e-5 of
+    sum |w x|, about ten times below what the matrix-core sums left behind
+    for such columns."""
+    torch = torch_cuda()
+    gen = synth.rng(7100 + kind)
+    in_dim = 1280
+    x = synth.activations_np(in_dim, gen)
+    x[17] *= np.float32(1e6)                              # column 0
+    x[256 + gen.permutation(256)[:16]] *= np.float32(1e4)  # column 1: 16 dominant
+    x[512 + gen.permutation(256)[:17]] *= np.float32(1e4)  # column 2: 17
+    x[768:1024] = 0.0                                     # column 3: three nonzero
+    x[768 + np.array([5, 77, 200])] = np.float32([3.0, -2.0, 1.5])
+    try:
+        for rows in (0, 1, 2):
+            dev.set_mfma_rows(rows)
+            for out_dim in (130, 4096):
+                w = synth.weight_np(kind, out_dim, in_dim, gen)
+                dp = torch.empty(dev.packed_bytes(kind, in_dim, out_dim), dtype=torch.uint8, device="cuda")
+                dw = to_dev(w)
+                dev.pack(kind, dw.data_ptr(), in_dim, out_dim, dp.data_ptr(), stream())
+                print(f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} rows mode {rows} "
+                      f"plan {dev.matvec_plan(kind, in_dim, out_dim)}", flush=True)
+                dx = to_dev(x)
+                dy = torch.full((out_dim,), float("nan"), dtype=torch.float32, device="cuda")
+                dev.matvec_packed(kind, dp.data_ptr(), in_dim, out_dim, dx.data_ptr(), dy.data_ptr(), stream())
+                sync()
+                want = oracle.qmatvec(kind, w, in_dim, out_dim, x, nthreads=ncpu())
+                r = assert_close_scaled(dy.cpu().numpy(), want, abs_dot_scale(kind, w, in_dim, out_dim, x),
+                                        rtol=3e-5, what=f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} rows {rows}")
+                print(f"  max err / sum|wx| = {r:.2e}", flush=True)
+    finally:
+        dev.set_mfma_rows(0)
 
 
 # Matrix-core matvec workgroup shapes forced (aspida_kq_set_mfma_rows: 64-row
