@@ -285,7 +285,8 @@ struct MvWorkspace {
 //   5-16 vectors: one pass;
 //   on matrices of at least MM16_TALL_UNITS pairs up to 16 vectors: the
 //     16-vector kernel (Q6_K up to 4 vectors: the batch-1 kernel on 4);
-//   above 16: one pass for Q6_K (launches of 32 vectors on 64-row tiles);
+//   above 16: one pass for Q6_K (launches of 32 vectors on 64-row tiles;
+//     above 32 on at most MMW_MAX_UNITS pairs the wave-per-column kernel);
 //     Q4_K on the 64-vector kernel in one launch.
 // The 16-vector kernel stays an engine of its own (3).
 constexpr int MULTI_MAX_BATCH = 8;
@@ -299,6 +300,7 @@ constexpr long MM16_MIN_UNITS = 2048;
 // at 14336x4096 (3584 pairs), the one-pass kernel is ahead (Q4_K 8 vectors
 // 15.2 against 19.1 us).
 constexpr long MM16_TALL_UNITS = 8192;
+constexpr long MMW_MAX_UNITS = 1024;
 // Test and tuning overrides (aspida_kq_set_*) are per calling thread: a
 // thread's override changes only the launches that thread makes.
 thread_local int g_mm_engine = 0;
@@ -326,6 +328,12 @@ MmRoute mm_route(int kind, int in_dim, int out_dim, int batch) {
   if (eng == 4 && kq::mmv_kind(kind)) return {3, 64};
   if (eng == 5 && kq::matvec_nv_takes(kind, in_dim, out_dim)) return {4, 4};
   if (eng == 6 && kq::mmw_takes(kind, in_dim)) return {5, 64};
+  // Q6_K above 32 vectors on at most MMW_MAX_UNITS (tile, column) pairs:
+  // the wave-per-column kernel in one launch (4096^2, 64 vectors: 32.8
+  // against 36.1 us for two 32-vector one-pass launches; at 14336x4096 the
+  // one-pass launches stay ahead, 86 against 95-110 us).
+  if (eng == 0 && kind == kq::Q6_K && batch > 32 && units <= MMW_MAX_UNITS && kq::mmw_takes(kind, in_dim))
+    return {5, 64};
   if (eng == 0 && kq::mmv_kind(kind) && kq::matvec_nv_takes(kind, in_dim, out_dim)) {
     // Very tall matrices (output heads): the 16-vector kernel, whose
     // activation pre-pass is amortised over many rows.

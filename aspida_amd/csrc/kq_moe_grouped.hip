@@ -238,13 +238,13 @@ __device__ __forceinline__ float moe1_unit(const MvCol<KIND, 1>& c, float4 xv, M
     if (lane < 17) sh.img[j][lane] = make_uint4(0u, 0u, 0u, 0u);
   const MvLane L = mv_lane<KIND>(sh.img, lane);
   float acc[1] = {0.f};
-  mv_column<KIND, 1, 17>(c, xv, L, sh.img, sh.xsum, (MvHdr<KIND>*)nullptr, lane, acc, grp, xs, rb0);
+  const bool taken = mv_column<KIND, 1, 17>(c, xv, L, sh.img, sh.xsum, (MvHdr<KIND>*)nullptr, lane, acc);
   float* red = reinterpret_cast<float*>(&sh.img[0][0]);
   __builtin_amdgcn_wave_barrier();
   red[lane] = acc[0];
   __builtin_amdgcn_wave_barrier();
   const float* rr = red + (lane & 15);
-  return ((rr[0] + rr[16]) + rr[32]) + rr[48];
+  return ((rr[0] + rr[16]) + rr[32]) + rr[48] + mv_dominant_exact<KIND, 1>(taken ? 1u : 0u, 1, grp, 0, xs, lane, rb0);
 }
 
 template <int KIND, int NW>

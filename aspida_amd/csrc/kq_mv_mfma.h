@@ -563,70 +563,100 @@ __device__ __forceinline__ void mv_dot(const MvCol<Q3_K, RB>& c, const uint4 (&i
 // would stay behind against a small sum |w x| (with one 10^4x activation:
 // up to 4.3e-4 of it for Q2_K, 2.6e-4 for Q6_K, 2.4e-4 for Q3_K; Q4_K and
 // Q5_K stay below 1e-4).  For Q2_K, Q3_K and Q6_K, a column where at most 16
-// activations are within 16x of its largest |x| has those activations
-// zeroed in the image and its sub-block sums, and each lane adds w x for them
-// in f32, w its row's dequantized weight read from the packed group
-// (dequant_elem, bit-exact); row r's terms go to lane (r % 16, 0)'s
-// accumulator of block r / 16.  Other columns pay only the test: four
+// activations are within 16x of its largest |x| (mv_dominant) has those
+// activations zeroed in the image and its sub-block sums; mv_column returns
+// true for it, and once its row sums are formed the wave adds w x for them
+// in f32 (mv_dominant_exact), w its row's dequantized weight read from the
+// packed group (dequant_elem, bit-exact).  Out of the column loop, the rare
+// exact part costs the loop no registers; other columns pay only the test: four
 // compares against max |x| / 16 and a count of the ballots (an ordinary
 // column has most of its 256 activations within 16x of its largest).
 template <int KIND> constexpr bool MV_EXACT_DOMINANT = KIND == Q2_K || KIND == Q3_K || KIND == Q6_K;
 
+// The dominant set of a column whose max |x| bits are mx: ballots per float4
+// component (bit l of bits[c] is element 4 l + c) and the test.  A
+// non-finite maximum makes thr infinite or NaN: no set is taken out unless
+// some |x| is infinite (their products are not finite either way).
+struct MvDominant {
+  uint64_t bits[4];
+  bool take;
+};
+__device__ __forceinline__ MvDominant mv_dominant(float4 xv, uint32_t mx) {
+  MvDominant d;
+  const float thr = __builtin_bit_cast(float, mx) * 0.0625f;
+  d.bits[0] = __ballot(__builtin_fabsf(xv.x) >= thr);
+  d.bits[1] = __ballot(__builtin_fabsf(xv.y) >= thr);
+  d.bits[2] = __ballot(__builtin_fabsf(xv.z) >= thr);
+  d.bits[3] = __ballot(__builtin_fabsf(xv.w) >= thr);
+  const int n = __builtin_popcountll(d.bits[0]) + __builtin_popcountll(d.bits[1]) +
+                __builtin_popcountll(d.bits[2]) + __builtin_popcountll(d.bits[3]);
+  d.take = __builtin_expect(n > 0 && n <= 16, 0);
+  return d;
+}
+
+// Returns whether the column's dominant activations were left out (the
+// caller adds them with mv_dominant_exact).
 template <int KIND, int RB, int IL = (RB == 4 ? 64 : 17)>
-__device__ __forceinline__ void mv_column(const MvCol<KIND, RB>& c, float4 xv, const MvLane& L,
+__device__ __forceinline__ bool mv_column(const MvCol<KIND, RB>& c, float4 xv, const MvLane& L,
                                           uint4 (&img)[8][IL], float* xsum, MvHdr<KIND>* hdr, int lane,
-                                          float (&acc)[RB], const uint8_t* grp, const float* xs, int rb0) {
+                                          float (&acc)[RB]) {
   __builtin_amdgcn_wave_barrier();
   uint32_t mx = wave_max_abs_bits(xv);
-  uint64_t bits[4] = {0u, 0u, 0u, 0u};
-  bool exact = false;
+  bool taken = false;
   if constexpr (MV_EXACT_DOMINANT<KIND>) {
-    // A non-finite maximum makes thr infinite or NaN: no dominant set is
-    // taken out unless some |x| is infinite (their products are not finite
-    // either way).
+    // mv_dominant's test, with the compares redone in the (rare) branch so
+    // that no lane mask lives across it.
     const float thr = __builtin_bit_cast(float, mx) * 0.0625f;
-    const bool dx = __builtin_fabsf(xv.x) >= thr, dy = __builtin_fabsf(xv.y) >= thr;
-    const bool dz = __builtin_fabsf(xv.z) >= thr, dw = __builtin_fabsf(xv.w) >= thr;
-    bits[0] = __ballot(dx);
-    bits[1] = __ballot(dy);
-    bits[2] = __ballot(dz);
-    bits[3] = __ballot(dw);
-    const int n = __builtin_popcountll(bits[0]) + __builtin_popcountll(bits[1]) + __builtin_popcountll(bits[2]) +
-                  __builtin_popcountll(bits[3]);
-    exact = __builtin_expect(n > 0 && n <= 16, 0);
-    if (exact) {
-      xv.x = dx ? 0.f : xv.x;
-      xv.y = dy ? 0.f : xv.y;
-      xv.z = dz ? 0.f : xv.z;
-      xv.w = dw ? 0.f : xv.w;
+    const int n = __builtin_popcountll(__ballot(__builtin_fabsf(xv.x) >= thr)) +
+                  __builtin_popcountll(__ballot(__builtin_fabsf(xv.y) >= thr)) +
+                  __builtin_popcountll(__ballot(__builtin_fabsf(xv.z) >= thr)) +
+                  __builtin_popcountll(__ballot(__builtin_fabsf(xv.w) >= thr));
+    if (__builtin_expect(n > 0 && n <= 16, 0)) {
+      xv.x = __builtin_fabsf(xv.x) >= thr ? 0.f : xv.x;
+      xv.y = __builtin_fabsf(xv.y) >= thr ? 0.f : xv.y;
+      xv.z = __builtin_fabsf(xv.z) >= thr ? 0.f : xv.z;
+      xv.w = __builtin_fabsf(xv.w) >= thr ? 0.f : xv.w;
       mx = wave_max_abs_bits(xv);
+      taken = true;
     }
   }
   const float invS = build_image<KIND>(xv, L, xsum, mx);
   mv_dot<RB, IL>(c, img, xsum, invS, L, hdr, lane, acc);
-  if (MV_EXACT_DOMINANT<KIND> && exact) {  // after the dot, when its registers are free
-    const PackedBytes<KIND> wr(grp, RB == 4 ? lane : 16 * rb0 + (lane & 15));
-    float t = 0.f;
-    // One dominant element at a time (bit i of component cpt's ballot is
-    // element 4 i + cpt): the loop stays rolled, so only one element's
-    // decode is live.
-    uint64_t m = bits[0];
-    int cpt = 0;
+  return taken;
+}
+
+// The exact part of the columns mv_column left dominant activations out of,
+// for the lane's output row (RB = 4: row `lane`; RB = 1: row 16 rb0 +
+// lane % 16).  Column s of the wave's run sits at xs0 + 256 s (activations)
+// and grp0 + s gstride (packed group); bit s % 64 of `hint` is set for every
+// such column, and each column s with its bit set is tested again (the same
+// test, so the same set) -- a run of more than 64 columns shares bits.
+template <int KIND, int RB>
+__device__ __forceinline__ float mv_dominant_exact(uint64_t hint, int spw, const uint8_t* grp0, size_t gstride,
+                                                   const float* xs0, int lane, int rb0) {
+  float t = 0.f;
+  if constexpr (MV_EXACT_DOMINANT<KIND>) {
 #pragma nounroll
-    while (true) {
-      while (m == 0 && cpt < 3) m = bits[++cpt];
-      if (m == 0) break;
-      const int e = 4 * (int)__builtin_ctzll(m) + cpt;
-      m &= m - 1;
-      t = __builtin_fmaf(dequant_elem<KIND>(wr, e), xs[e], t);
-    }
-    const bool g0 = (lane >> 4) == 0;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const float u = RB == 4 ? __shfl(t, 16 * rb + (lane & 15), 64) : t;
-      if (g0) acc[rb] += u;
+    for (uint64_t h = hint; h; h &= h - 1) {
+#pragma nounroll
+      for (int s = (int)__builtin_ctzll(h); s < spw; s += 64) {
+        const float* xs = xs0 + (size_t)s * 256;
+        float4 xv;
+        __builtin_memcpy(&xv, __builtin_assume_aligned(xs + 4 * lane, 16), 16);
+        const MvDominant d = mv_dominant(xv, wave_max_abs_bits(xv));
+        if (!d.take) continue;
+        const PackedBytes<KIND> wr(grp0 + (size_t)s * gstride, RB == 4 ? lane : 16 * rb0 + (lane & 15));
+#pragma nounroll
+        for (int cpt = 0; cpt < 4; ++cpt)
+#pragma nounroll
+          for (uint64_t m = d.bits[cpt]; m; m &= m - 1) {
+            const int e = 4 * (int)__builtin_ctzll(m) + cpt;  // element e of the column
+            t = __builtin_fmaf(dequant_elem<KIND>(wr, e), xs[e], t);
+          }
+      }
     }
   }
+  return t;
 }
 
 // The LDS one wave uses: its A image, sub-block sums and row headers.
@@ -682,8 +712,9 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
   float acc[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) acc[rb] = 0.f;
+  uint64_t hint = 0;  // bit s % 64: column s left dominant activations to mv_dominant_exact
   if (PIPE == MV_ONE) {
-    mv_column(c0, x0, L, img, xsum, hdr, lane, acc, gp, xc, rb0);
+    hint |= (uint64_t)mv_column(c0, x0, L, img, xsum, hdr, lane, acc);
   } else if (PIPE == MV_SEQ) {  // columns one after another: one register set, more waves per CU
     for (int s = 0; s < spw; ++s) {
       if (s > 0) {
@@ -691,7 +722,7 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
         __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)s * 256, 16), 16);
         c0.load(gp + (size_t)s * GB, lane, rb0);
       }
-      mv_column(c0, x0, L, img, xsum, hdr, lane, acc, gp + (size_t)s * GB, xc + (size_t)s * 256, rb0);
+      hint |= (uint64_t)mv_column(c0, x0, L, img, xsum, hdr, lane, acc) << (s & 63);
     }
   } else {
     // Two register sets used in turn: the next column's loads are in flight
@@ -703,26 +734,27 @@ __device__ __forceinline__ float mv_mfma_rows(const uint8_t* __restrict__ P, int
       __builtin_memcpy(&x1, __builtin_assume_aligned(xp + (size_t)s1 * 256, 16), 16);
       c1.load(gp + (size_t)s1 * GB, lane, rb0);
       asm volatile("" ::: "memory");  // keep these loads issued here
-      mv_column(c0, x0, L, img, xsum, hdr, lane, acc, gp + (size_t)s * GB, xc + (size_t)s * 256, rb0);
+      hint |= (uint64_t)mv_column(c0, x0, L, img, xsum, hdr, lane, acc) << (s & 63);
       if (s + 2 < spw) {
         __builtin_memcpy(&x0, __builtin_assume_aligned(xp + (size_t)(s + 2) * 256, 16), 16);
         c0.load(gp + (size_t)(s + 2) * GB, lane, rb0);
         asm volatile("" ::: "memory");
       }
-      if (s + 1 < spw)
-        mv_column(c1, x1, L, img, xsum, hdr, lane, acc, gp + (size_t)s1 * GB, xc + (size_t)s1 * 256, rb0);
+      if (s + 1 < spw) hint |= (uint64_t)mv_column(c1, x1, L, img, xsum, hdr, lane, acc) << (s1 & 63);
     }
   }
 
   // Lane (n, g) holds rows 16 rb + n over its quarter: add the four quarters
-  // (ascending g).
+  // (ascending g), then the dominant activations' exact terms of the lane's
+  // row.
   float* red = reinterpret_cast<float*>(&img[0][0]);
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) red[rb * 64 + lane] = acc[rb];
   __builtin_amdgcn_wave_barrier();
   const float* rr = red + (RB == 4 ? (lane >> 4) * 64 : 0) + (lane & 15);
-  return ((rr[0] + rr[16]) + rr[32]) + rr[48];
+  const float y = ((rr[0] + rr[16]) + rr[32]) + rr[48];
+  return y + mv_dominant_exact<KIND, RB>(hint, PIPE == MV_ONE ? 1 : spw, gp, GB, xc, lane, rb0);
 }
 
 __device__ __forceinline__ float4 ld_f4(const float* p) {
@@ -761,6 +793,9 @@ __device__ __forceinline__ void mv_mfma_rows_nv(const uint8_t* __restrict__ P, i
   for (int v = 0; v < NV; ++v)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[v][rb] = 0.f;
+  uint64_t hint[NV];  // per vector, as in mv_mfma_rows
+#pragma unroll
+  for (int v = 0; v < NV; ++v) hint[v] = 0;
   for (int s = 0; s < spw; ++s) {
     if (s > 0) {
       asm volatile("" ::: "memory");  // the next column's loads stay after this column's work
@@ -769,10 +804,9 @@ __device__ __forceinline__ void mv_mfma_rows_nv(const uint8_t* __restrict__ P, i
       c0.load(gp + (size_t)s * GB, lane, rb0);
     }
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
-      mv_column(c0, xv[v], L, img, xsum, hdr, lane, acc[v], gp + (size_t)s * GB,
-                x + (size_t)(v < nv ? v : nv - 1) * ldx + (size_t)(sb0 + s) * 256, rb0);
+    for (int v = 0; v < NV; ++v) hint[v] |= (uint64_t)mv_column(c0, xv[v], L, img, xsum, hdr, lane, acc[v]) << (s & 63);
   }
+
   // Lane (n, g) holds rows 16 rb + n over its quarter: add the four quarters
   // (ascending g), vector by vector.
   float* red = reinterpret_cast<float*>(&img[0][0]);
@@ -783,7 +817,9 @@ __device__ __forceinline__ void mv_mfma_rows_nv(const uint8_t* __restrict__ P, i
     for (int rb = 0; rb < RB; ++rb) red[rb * 64 + lane] = acc[v][rb];
     __builtin_amdgcn_wave_barrier();
     const float* rr = red + (RB == 4 ? (lane >> 4) * 64 : 0) + (lane & 15);
-    out[v] = ((rr[0] + rr[16]) + rr[32]) + rr[48];
+    out[v] = ((rr[0] + rr[16]) + rr[32]) + rr[48] +
+             mv_dominant_exact<KIND, RB>(hint[v], spw, gp, GB,
+                                         x + (size_t)(v < nv ? v : nv - 1) * ldx + (size_t)sb0 * 256, lane, rb0);
   }
 }
 

@@ -116,9 +116,17 @@ __device__ __forceinline__ void mv16_epilogue(float r, int blk, int out_rows, fl
   if (lane < 16 && row < out_rows) y[row] = r;
 }
 
+// Six waves per SIMD for the Q6_K 16-row kernels of 8 or more waves walking
+// their columns one after another (the output head's plan: three 8-wave
+// workgroups per CU), which the registers of the dominant-activation path
+// (kq_mv_mfma.h) would otherwise cut to five (head 65 -> 75 us); they fit
+// without spilling (79 VGPRs).  Q3_K would spill and keeps five.
+constexpr int mv16_waves(int kind, int nw, int pipe) { return kind == Q6_K && nw >= 8 && pipe == MV_SEQ ? 6 : 1; }
+
 template <int KIND, int NW, int PIPE>
-__global__ __launch_bounds__(64 * NW) void kq_mv_mfma16(const uint8_t* __restrict__ P, int nsb, int out_rows,
-                                                       const float* __restrict__ x, float* __restrict__ y, int spw) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(mv16_waves(KIND, NW, PIPE))))
+void kq_mv_mfma16(const uint8_t* __restrict__ P, int nsb, int out_rows, const float* __restrict__ x,
+                  float* __restrict__ y, int spw) {
   __shared__ MvShared16 sh[NW];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -115,6 +115,8 @@ def parse():
                          "the persistent matvec chain experiment beside the decode")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
+    ap.add_argument("--mm-engine", type=int, choices=[0, 1, 2, 3, 4, 5, 6], default=0,
+                    help="small-batch engine for the 'small' table (aspida_kq_set_mm_engine): 0 = the library's pick")
     ap.add_argument("--no-70b", action="store_true", help="skip the Llama-3-70B weight-stream line")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run one device copy of this many MiB (calibrates rocprofv3 byte counters)")
@@ -338,13 +340,14 @@ def kquant_table(torch, aa, synth, seed, stream, shapes=None):
     return table
 
 
-def small_batch_table(torch, aa, synth, seed, stream):
+def small_batch_table(torch, aa, synth, seed, stream, engine=0):
     """Small-batch products: Q4_K and Q6_K at 4096x4096 and
     14336x4096 for B in {2, 4, 8, 16, 32, 64}, packed weights (the library's
     pick per kind, shape and batch: small_batch_kernel), launches rotating
     over >= 1 GiB of weight copies.  GB/s counts W + 4 B (in + out) bytes;
     TFLOP/s counts 2 B in out."""
     dev = aa.DeviceOps()
+    dev.set_mm_engine(engine)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 2)
     table = {}
@@ -381,7 +384,7 @@ def small_batch_table(torch, aa, synth, seed, stream):
                 t = e0.elapsed_time(e1) * 1e-3 / (3 * ncopy)
                 nbytes = aa.weight_bytes(kind, inp, out) + 4 * B * (inp + out)
                 table[f"{aa.KIND_NAMES[kind]} {out}x{inp} B={B}"] = {
-                    "kernel": small_batch_kernel(aa, kind, inp, out, B),
+                    "kernel": small_batch_kernel(aa, kind, inp, out, B) if engine == 0 else f"engine {engine}",
                     "us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
                     "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3),
                     "TFLOPs": round(2.0 * B * inp * out / t / 1e12, 2)}
@@ -390,6 +393,7 @@ def small_batch_table(torch, aa, synth, seed, stream):
                 del graph
             del P
             torch.cuda.empty_cache()
+    dev.set_mm_engine(0)
     return table
 
 
@@ -398,8 +402,12 @@ def small_batch_kernel(aa, kind, inp, out, B):
     aspidagpu.hip) for Q4_K and Q6_K: up to 4 vectors the batch-1 kernel on
     4 vectors where the batch-1 plan is 16-row workgroups (and Q6_K at 2),
     else the one-pass kernel; the one-pass kernel up to 16 vectors and for
-    Q6_K above; Q4_K above 16 on the 64-vector MFMA kernel."""
-    tall = (-(-out // 64)) * (inp // 256) >= 8192
+    Q6_K above (the wave-per-column kernel above 32 vectors on at most 1024
+    (tile, column) pairs); Q4_K above 16 on the 64-vector MFMA kernel."""
+    units = (-(-out // 64)) * (inp // 256)
+    tall = units >= 8192
+    if kind == aa.Q6_K and B > 32 and units <= 1024 and inp % 1024 == 0:
+        return "kq_mmw"
     if B <= 4:
         if tall:
             return "kq_mv_mfma16n" if kind == aa.Q6_K else "kq_mm16_q4k"
@@ -721,8 +729,9 @@ def small_batch_spot_check(torch, aa, named, gen, threads):
     """Ties the small_batch table's kernels to the oracle: each small-batch
     kernel family the library picks at the table's shapes (small_batch_kernel)
     runs once through the same entry point (aspida_kq_matmul_packed_dev) --
-    Q4_K 4096 x 4096 (the baseline's own o) at B = 2, 8 and 64, and a Q6_K
-    14336 x 4096 matrix at B = 2, 16 and 64 -- and 64 sampled rows of every
+    Q4_K 4096 x 4096 (the baseline's own o) at B = 2, 8 and 64, a Q6_K
+    14336 x 4096 matrix at B = 2, 16 and 64 and a Q6_K 4096 x 4096 one at
+    B = 64 -- and 64 sampled rows of every
     vector's output are compared with QMatVec (llm_dequant.adb:808-932) within
     1e-4 * sum_i |w_i x_i|.  Exits if any is out."""
     import numpy as np
@@ -730,8 +739,9 @@ def small_batch_spot_check(torch, aa, named, gen, threads):
     from aspida_amd import synth
     dev = aa.DeviceOps()
     q6 = synth.weight_np(Q6_K, FFN, HIDDEN, gen)
+    q6s = synth.weight_np(Q6_K, HIDDEN, HIDDEN, gen)
     cases = [(Q4_K, named["o"][1], HIDDEN, HIDDEN, b) for b in (2, 8, 64)] + \
-            [(Q6_K, q6, FFN, HIDDEN, b) for b in (2, 16, 64)]
+            [(Q6_K, q6, FFN, HIDDEN, b) for b in (2, 16, 64)] + [(Q6_K, q6s, HIDDEN, HIDDEN, 64)]
     worst = {}
     for kind, w, out, inp, B in cases:
         raw = torch.from_numpy(np.ascontiguousarray(w)).cuda()
@@ -963,8 +973,11 @@ def main():
             print(json.dumps({"moe_prefill": moe_table(torch, aa, synth, args.seed, stream, PREFILL_TOKENS,
                                                         "MoE prefill")}), flush=True)
             return
-        fn = {"small": small_batch_table, "moe": moe_table, "kquant": kquant_table,
-              "sweep": size_sweep_table}[args.only]
+        if args.only == "small":
+            print(json.dumps({"small": small_batch_table(torch, aa, synth, args.seed, stream, args.mm_engine)}),
+                  flush=True)
+            return
+        fn = {"moe": moe_table, "kquant": kquant_table, "sweep": size_sweep_table}[args.only]
         print(json.dumps({args.only: fn(torch, aa, synth, args.seed, stream)}), flush=True)
         return
     dec = Decoder(torch, aa, synth, args.seed, args.mv_engine)

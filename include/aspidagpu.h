@@ -415,7 +415,8 @@ int aspida_kq_set_mv_engine(int engine);
  * 16 vectors (on matrices of at least 8192 64-row-by-256-column blocks,
  * such as output heads, the 16-vector matrix-core kernel instead, Q6_K from
  * 5 vectors); above 16 the one-pass kernel for Q6_K -- in launches of 32
- * vectors where it takes 64-row tiles -- and the 64-vector matrix-core
+ * vectors where it takes 64-row tiles; above 32 vectors on at most 1024
+ * such blocks the wave-per-column kernel (6) -- and the 64-vector matrix-core
  * kernel for Q4_K; other kinds on the vector kernel); 1 = the vector kernel; 2 = the 64-vector and 3 = the
  * 16-vector matrix-core kernel; 4 = the one-pass matrix-core kernel (up to
  * 64 vectors per weight pass); 5 = the batch-1 matrix-core kernel on up to 4
