@@ -149,7 +149,6 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
   i = __builtin_amdgcn_readlane(i, 63);
 }
-#endif
 
 // The bits of the largest |x| over the wave's float4s, in every lane.
 // Non-negative floats order as their bit patterns do, so the reduction is an
@@ -167,6 +166,7 @@ __device__ __forceinline__ uint32_t wave_max_abs_bits(float4 v) {
   m = step(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x143, 0xC, 0xF, true));
   return (uint32_t)__builtin_amdgcn_readlane((int)m, 63);
 }
+#endif
 
 
 }  // namespace kq

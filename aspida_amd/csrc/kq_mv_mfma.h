@@ -646,10 +646,13 @@ __device__ __forceinline__ float mv_dominant_exact(uint64_t hint, int spw, const
         const MvDominant d = mv_dominant(xv, wave_max_abs_bits(xv));
         if (!d.take) continue;
         const PackedBytes<KIND> wr(grp0 + (size_t)s * gstride, RB == 4 ? lane : 16 * rb0 + (lane & 15));
+        // The component's ballot by selects: an indexed d.bits[cpt] would be
+        // a private array, which the compiler places in LDS (40 B a thread).
 #pragma nounroll
         for (int cpt = 0; cpt < 4; ++cpt)
 #pragma nounroll
-          for (uint64_t m = d.bits[cpt]; m; m &= m - 1) {
+          for (uint64_t m = cpt == 0 ? d.bits[0] : cpt == 1 ? d.bits[1] : cpt == 2 ? d.bits[2] : d.bits[3]; m;
+               m &= m - 1) {
             const int e = 4 * (int)__builtin_ctzll(m) + cpt;  // element e of the column
             t = __builtin_fmaf(dequant_elem<KIND>(wr, e), xs[e], t);
           }
