@@ -190,7 +190,8 @@ __global__ __launch_bounds__(64 * NW) void moe_down(MoeGroupedArgs a, int cpw, c
 //                 pair of those rows, NW waves over the pairs, and forms
 //                 y = sum_k top_w[k] y_k (ascending k) + g_t y_shared in LDS
 //                 (llm_moe.adb:270-299).
-// Expert ids outside [0, n_exp) are clamped.
+// Expert ids outside [0, n_exp) are clamped for the loads, and such a
+// token's y is not written.
 constexpr int MOE1_MAX_UNITS = 64;  // (slot, down column) pairs per down workgroup
 
 __device__ __forceinline__ int moe_expert(const MoeGroupedArgs& a, int k) {
@@ -253,11 +254,13 @@ __global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
   __shared__ MvShared16 sh[NW];
   __shared__ float part[MOE1_MAX_UNITS][16];
   __shared__ float wk[MOE_MAX_TOPK + 1];  // the combine's slot weights, top_w[k] and g last
+  __shared__ int ids[MOE_MAX_TOPK];       // the slots' expert ids (a token with an invalid one keeps y unwritten)
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = blockIdx.x, nsb = a.I / 256, units = (a.top_k + 1) * nsb;
   // Requested now, with the first loads, rather than one after another in the combine.
   if ((int)threadIdx.x <= a.top_k) wk[threadIdx.x] = (int)threadIdx.x < a.top_k ? a.top_w[threadIdx.x] : a.gsh[0];
+  if ((int)threadIdx.x < a.top_k) ids[threadIdx.x] = a.idx[threadIdx.x];
   // Units u and u + NW of a wave: both units' weights and activations are
   // requested before either is multiplied, so their loads overlap.
   for (int u = w; u < units; u += 2 * NW) {
@@ -283,12 +286,14 @@ __global__ __launch_bounds__(64 * NW) void moe_down1(MoeGroupedArgs a) {
   if (threadIdx.x < 16) {
     const int t = threadIdx.x;
     float acc = 0.f;
+    bool valid = true;
     for (int k = 0; k <= a.top_k; ++k) {
       float s = 0.f;
       for (int c = 0; c < nsb; ++c) s += part[k * nsb + c][t];
       acc = acc + wk[k] * s;
+      if (k < a.top_k) valid = valid && ids[k] >= 0 && ids[k] < a.n_exp;
     }
-    a.y[16 * b + t] = acc;
+    if (valid) a.y[16 * b + t] = acc;
   }
 }
 

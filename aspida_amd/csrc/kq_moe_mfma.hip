@@ -496,7 +496,8 @@ __global__ __launch_bounds__(MR_THREADS * HW) void moe_down_mf(MoeGroupedArgs a)
 
 // y[t][row] = sum_k top_w[t][k] yk[t slots + k][row] (ascending k) +
 // g_t yk[t slots + top_k][row] (llm_moe.adb:270-299); one thread per
-// (token, row), yk loads batched eight at a time.
+// (token, row), yk loads batched eight at a time.  A token with an expert id
+// outside [0, n_exp) had a job the schedule dropped: its y is not written.
 __global__ __launch_bounds__(256) void moe_combine_mf(MoeGroupedArgs a) {
   const int row = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
   if (row >= a.dim) return;
@@ -504,19 +505,24 @@ __global__ __launch_bounds__(256) void moe_combine_mf(MoeGroupedArgs a) {
   const float* yt = a.yk + (size_t)t * slots * a.dim + row;
   const float vs = yt[(size_t)a.top_k * a.dim], gs = a.gsh[t];
   float acc = 0.f;
+  bool valid = true;
   for (int k0 = 0; k0 < a.top_k; k0 += 8) {
     float v[8], wk[8];
+    int e[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int k = k0 + i < a.top_k ? k0 + i : k0;
       v[i] = yt[(size_t)k * a.dim];
       wk[i] = a.top_w[t * a.top_k + k];
+      e[i] = a.idx[t * a.top_k + k];
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
       if (k0 + i < a.top_k) acc = acc + wk[i] * v[i];
+      valid = valid && e[i] >= 0 && e[i] < a.n_exp;
+    }
   }
-  a.y[(size_t)t * a.dim + row] = acc + gs * vs;
+  if (valid) a.y[(size_t)t * a.dim + row] = acc + gs * vs;
 }
 
 // ---- launchers ------------------------------------------------------------------

@@ -36,9 +36,32 @@ import re
 import statistics
 
 
+def _unmangle(name):
+    """'_ZN2kq9kq_xsplitILi32EEEvPKf...' -> 'kq_xsplit<32>': the last name of an
+    Itanium nested name and its integer / bool template arguments (the profiler
+    leaves names mangled when it cannot demangle a parameter type, _Float16)."""
+    i, ident = 3, None
+    while i < len(name) and name[i].isdigit():
+        j = i
+        while name[j].isdigit():
+            j += 1
+        n = int(name[i:j])
+        ident, i = name[j:j + n], j + n
+    if ident is None:
+        return name
+    args = []
+    if i < len(name) and name[i] == "I":
+        for m in re.finditer(r"L([ib])(n?\d+)E", name[i + 1:name.find("EE", i) + 1]):
+            v = m.group(2).replace("n", "-")
+            args.append(("true" if v == "1" else "false") if m.group(1) == "b" else v)
+    return ident + (f"<{', '.join(args)}>" if args else "")
+
+
 def short_name(name):
     """'void kq::kq_mv_packed<0, 16>(unsigned char const*, ...)' -> 'kq_mv_packed<0, 16>'
-    ('(anonymous namespace)::' scopes dropped first)."""
+    ('(anonymous namespace)::' scopes dropped first); mangled names by _unmangle."""
+    if name.startswith("_ZN"):
+        return _unmangle(name)
     head = name.replace("(anonymous namespace)::", "").split("(")[0]
     head = re.sub(r"^void\s+", "", head)
     return head.split("::")[-1] if "::" in head else head
@@ -230,14 +253,17 @@ def bench_rows_pmc(table, trace_csv, pmc_csv):
     print("| row | kernel | µs | GB/s | " + " | ".join(names) + " | VALU busy | MFMA busy |")
     print("|---|---|---|---|" + "---|" * len(names) + "---|---|")
     for r, (kind, o, i, b) in enumerate(spec):
-        us = statistics.median(v for _, v in tr[r])
-        mean = {n: statistics.fmean(v for _, v in pm[n][r]) for n in names}
-        nbytes = _BLOCK[kind] * o * (i // 256) + 4 * (i + o)
-        cyc = SIMDS * us * CLOCK_MHZ
-        valu = (mean.get("SQ_INSTS_VALU", 0.0) - mean.get("SQ_INSTS_MFMA", 0.0)) * VALU_CYCLES / cyc
-        mfma = mean.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / cyc
-        print(f"| {kind} {o}x{i} | {tr[r][0][0]} | {us:.2f} | {nbytes / us / 1e3:.0f} | " +
-              " | ".join(f"{mean[n]:.0f}" for n in names) + f" | {valu:.2f} | {mfma:.2f} |")
+        label = f"{kind} {o}x{i}" + (f" B={b}" if table == "small" else "")
+        nbytes = _BLOCK[kind] * o * (i // 256) + 4 * b * (i + o)
+        # one line per kernel of the row (a pre-pass and its product apart)
+        for kn in dict.fromkeys(n for n, _ in tr[r]):
+            us = statistics.median(v for n, v in tr[r] if n == kn)
+            mean = {c: statistics.fmean(v for n, v in pm[c][r] if n == kn) for c in names}
+            cyc = SIMDS * us * CLOCK_MHZ
+            valu = (mean.get("SQ_INSTS_VALU", 0.0) - mean.get("SQ_INSTS_MFMA", 0.0)) * VALU_CYCLES / cyc
+            mfma = mean.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / cyc
+            print(f"| {label} | {kn} | {us:.2f} | {nbytes / us / 1e3:.0f} | " +
+                  " | ".join(f"{mean[c]:.0f}" for c in names) + f" | {valu:.2f} | {mfma:.2f} |")
 
 
 def main():

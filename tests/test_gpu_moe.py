@@ -383,6 +383,50 @@ def test_moe_experts_packed_repeated_expert():
         _assert_moe(y[t], want, f"token {t}")
 
 
+@pytest.mark.parametrize("gk,dk", [(aa.Q4_K, aa.Q6_K), (aa.Q5_K, aa.Q3_K)], ids=["mfma", "valu"])
+def test_moe_experts_packed_invalid_expert(gk, dk):
+    """The grouped launches for 2..95 tokens: a token with an expert id outside
+    [0, n_exp) keeps its y unwritten (its job is never scheduled, so its
+    slots never all arrive), and every other token is still right."""
+    dim, inter, n_exp, top_k, T = 512, 768, 8, 3, 12
+    dev = aa.DeviceOps()
+    gen = synth.rng(1999)
+    L = _layer(gen, dim, inter, n_exp, gk, gk, dk)
+    X = synth.activations_np(T * dim, gen).reshape(T, dim)
+    idx = np.zeros((T, top_k), np.int32)
+    tw = np.zeros((T, top_k), np.float32)
+    for t in range(T):
+        idx[t], tw[t] = oracle.route(gen.standard_normal(n_exp).astype(np.float32), top_k)
+    idx[4] = [1, n_exp + 2, 0]
+    idx[7] = [-1, 2, 3]
+    y1, y2 = _run_packed(dev, L, dim, inter, n_exp, top_k, gk, dk, True, X, idx, tw)
+    for t in (4, 7):
+        assert np.all(np.isnan(y1[t])) and np.all(np.isnan(y2[t])), f"token {t} with an invalid expert was written"
+    for t in (0, 3, 5, 11):
+        want = oracle.moe_experts(X[t], dim, top_k, inter, n_exp, idx[t], tw[t], L["gate"], L["up"], L["down"],
+                                  L["shg"], L["shu"], L["shd"], shared_gate_inp=L["sgi"], nthreads=ncpu())
+        _assert_moe(y1[t], want, f"token {t}")
+
+
+def test_moe_experts_packed_invalid_expert_one_token():
+    """The one-token launches: an expert id outside [0, n_exp) leaves y
+    unwritten; a valid token's y is the oracle's."""
+    dim, inter, n_exp, top_k = 512, 768, 8, 3
+    dev = aa.DeviceOps()
+    gen = synth.rng(2003)
+    L = _layer(gen, dim, inter, n_exp)
+    X = synth.activations_np(dim, gen).reshape(1, dim)
+    tw = np.array([[0.5, 0.3, 0.2]], np.float32)
+    y, _ = _run_packed(dev, L, dim, inter, n_exp, top_k, aa.Q4_K, aa.Q6_K, True, X,
+                       np.array([[1, n_exp + 2, 0]], np.int32), tw)
+    assert np.all(np.isnan(y[0])), "a token with an invalid expert was written"
+    idx = np.array([[1, 5, 0]], np.int32)
+    y, _ = _run_packed(dev, L, dim, inter, n_exp, top_k, aa.Q4_K, aa.Q6_K, True, X, idx, tw)
+    want = oracle.moe_experts(X[0], dim, top_k, inter, n_exp, idx[0], tw[0], L["gate"], L["up"], L["down"],
+                              L["shg"], L["shu"], L["shd"], shared_gate_inp=L["sgi"], nthreads=ncpu())
+    _assert_moe(y[0], want, "token 0")
+
+
 
 def test_moe_prefill_repeated_and_invalid_experts():
     """The prefill products (T >= 96): a token that lists one expert twice gets
