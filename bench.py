@@ -583,10 +583,13 @@ def abi_path(aa, synth, seed, tokens=4):
             w = synth.weight_np(kind, out, inp, gen)
             x = synth.activations_np(inp, gen)
             gpu.matvec(w, kind, inp, out, x)
+            y = np.empty(out, np.float32)
+            fn, args = gpu.lib.aspida_gpu_matvec, (w.ctypes.data, w.nbytes, kind, inp, out, x.ctypes.data,
+                                                   y.ctypes.data)
             ts = []
             for _ in range(30):
                 t0 = time.perf_counter()
-                gpu.matvec(w, kind, inp, out, x)
+                fn(*args)
                 ts.append(time.perf_counter() - t0)
             assert gpu.last_error() == 0
             gpu.free_weight(w)
@@ -600,11 +603,19 @@ def abi_path(aa, synth, seed, tokens=4):
     head = synth.weight_np(Q6_K, VOCAB, HIDDEN, gen)
     xs = {HIDDEN: synth.activations_np(HIDDEN, gen), FFN: synth.activations_np(FFN, gen)}
 
+    # The calls with their arguments converted once, as a compiled caller
+    # passes them (ctypes' per-call conversion of numpy buffers would add
+    # about 5 us per call on the host, none of it the library's).
+    ys = {n: np.empty(n, np.float32) for n in (HIDDEN, KV, FFN, VOCAB)}
+    fn = gpu.lib.aspida_gpu_matvec
+    calls_args = [(w.ctypes.data, w.nbytes, kind, inp, out, xs[inp].ctypes.data, ys[out].ctypes.data)
+                  for ws in layers for (kind, out, inp), w in zip(plan, ws)]
+    calls_args.append((head.ctypes.data, head.nbytes, Q6_K, HIDDEN, VOCAB, xs[HIDDEN].ctypes.data,
+                       ys[VOCAB].ctypes.data))
+
     def token():
-        for ws in layers:
-            for (kind, out, inp), w in zip(plan, ws):
-                gpu.matvec(w, kind, inp, out, xs[inp])
-        gpu.matvec(head, Q6_K, HIDDEN, VOCAB, xs[HIDDEN])
+        for a in calls_args:
+            fn(*a)
 
     token()                                          # mirrors every weight into HBM
     t0 = time.perf_counter()
