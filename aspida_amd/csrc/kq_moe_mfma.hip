@@ -1,11 +1,13 @@
 // kq_moe_mfma.hip -- the grouped MoE experts on the matrix cores, for any
-// number of tokens T >= 2 with Q4_K or Q6_K projections.  Four launches:
+// number of tokens T >= 2 with Q4_K or Q6_K projections.  Three launches:
 //
-//   moe_plan_mf     one workgroup: the schedule (kq_moe_sched.h: jobs
-//                   bucketed per expert, shared expert first) cut into chunks
-//                   of up to MR_J jobs.
-//   moe_gate_up_mf  h[job][row] = silu(gate . x_t) * (up . x_t)
-//                   (llm_moe.adb:124-132); then the shared-expert gate
+//   moe_gate_up_mf  every workgroup first derives the schedule
+//                   (kq_moe_sched.h: jobs bucketed per expert, shared expert
+//                   first) in LDS, cut into chunks of up to MR_J jobs, and
+//                   keeps its own units' chunks; workgroup 0 publishes the
+//                   chunk table for the down launch.  Then
+//                   h[job][row] = silu(gate . x_t) * (up . x_t)
+//                   (llm_moe.adb:124-132), then the shared-expert gate
 //                   g_t = sigmoid(shared_gate_inp . x_t) (llm_moe.adb:285-293).
 //   moe_down_mf     yk[job][row] = down . h[job].
 //   moe_combine_mf  y = sum_k top_w[k] yk[k] (ascending k) + g_t yk[top_k]
@@ -50,26 +52,24 @@ struct MrImg {
   float pad[3];
 };
 
-// ---- plan -------------------------------------------------------------------------
+// ---- the schedule ---------------------------------------------------------------
 
-// a.units[0].x = the chunk count; a.units[1 + c] = chunk c: {expert, job 0,
-// job 1 or -1}.  Chunks are numbered position-major (kq_moe_sched.h).
-__global__ __launch_bounds__(1024) void moe_plan_mf(MoeGroupedArgs a) {
-  __shared__ MoeSched S;
-  const int chunks = moe_schedule<MR_J>(a, S);
-  const int ne = a.n_exp + 1;
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
-    int lo = 0, hi = ne - 1;  // the position p with coff[p] <= c < coff[p + 1]
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (S.coff[mid] <= c) lo = mid;
-      else hi = mid - 1;
-    }
-    const int j = S.joff[lo] + (c - S.coff[lo]) * MR_J;
-    a.units[1 + c] = make_int4(moe_expert_at(lo, a.n_exp), S.jobs[j], j + 1 < S.joff[lo + 1] ? S.jobs[j + 1] : -1, 0);
+// Chunk c of the schedule S (chunks are numbered position-major,
+// kq_moe_sched.h): {expert, job, job or -1, 0}.
+__device__ __forceinline__ int4 mr_chunk_entry(const MoeSched& S, int c, int n_exp) {
+  int lo = 0, hi = n_exp;  // the position p with coff[p] <= c < coff[p + 1]
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (S.coff[mid] <= c) lo = mid;
+    else hi = mid - 1;
   }
-  if (threadIdx.x == 0) a.units[0] = make_int4(chunks, 0, 0, 0);
+  const int j = S.joff[lo] + (c - S.coff[lo]) * MR_J;
+  return make_int4(moe_expert_at(lo, n_exp), S.jobs[j], j + 1 < S.joff[lo + 1] ? S.jobs[j + 1] : -1, 0);
 }
+
+// Units a gate/up workgroup takes at most (its grid is sized for it): their
+// chunks are kept in LDS once the schedule's tables are overwritten.
+constexpr int MR_UNITS_MAX = 32;
 
 // ---- shared pieces of the two expert launches -------------------------------------
 
@@ -300,20 +300,34 @@ __device__ __forceinline__ int mr_next_col(int s, bool last, int rot, int rotN, 
 template <int KIND>
 __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
   constexpr int NWV = 4;
-  __shared__ MrImg img[MR_J][MR_GC];
+  // The schedule's tables, then (once this workgroup's chunks are copied out)
+  // the activation images.
+  constexpr size_t LDS = sizeof(MrImg) * MR_J * MR_GC > sizeof(MoeSched) ? sizeof(MrImg) * MR_J * MR_GC
+                                                                          : sizeof(MoeSched);
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS];
+  __shared__ int4 mine[MR_UNITS_MAX];
+  MoeSched& S = *reinterpret_cast<MoeSched*>(lds);
+  MrImg(&img)[MR_J][MR_GC] = *reinterpret_cast<MrImg(*)[MR_J][MR_GC]>(lds);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int slots = a.top_k + 1, nsb = a.dim / 256, tiles = a.I / 64;
   constexpr int GB = 64 * Block<KIND>::BYTES;
-  // The unit count and this workgroup's first chunk are read together (the
-  // grid never exceeds the table's chunk bound times the tiles).
-  int u = blockIdx.x;
-  const int4 C = mr_chunk(a, 1 + u / tiles);
-  const int units = mr_chunk(a, 0).x * tiles;
+  const int units = moe_schedule<MR_J>(a, S) * tiles;
+  if (blockIdx.x == 0) {  // the chunk table of the down launch
+    for (int c = threadIdx.x; c < units / tiles; c += blockDim.x) a.units[1 + c] = mr_chunk_entry(S, c, a.n_exp);
+    if (threadIdx.x == 0) a.units[0] = make_int4(units / tiles, 0, 0, 0);
+  }
+  for (int k = threadIdx.x; k < MR_UNITS_MAX; k += blockDim.x) {
+    const int uk = blockIdx.x + k * (int)gridDim.x;
+    if (uk < units) mine[k] = mr_chunk_entry(S, uk / tiles, a.n_exp);
+  }
+  __syncthreads();  // the tables are no longer read: the LDS takes the images
+  int u = blockIdx.x, k = 0;
   if (u >= units) {
     mr_housekeeping<NWV>(a, w, lane);
     return;
   }
+  const int4 C = mine[0];
   const auto gbase = [&](const MrUnit& V, const uint8_t* routed, const uint8_t* sh) {
     return (V.e == a.n_exp ? sh : routed + (size_t)V.e * a.gu_stride) + (size_t)V.tile * nsb * GB;
   };
@@ -336,7 +350,7 @@ __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
     // The next unit (this one again after the last: its loads go unused).
     const int un = u + (int)gridDim.x;
     const bool more = un < units;
-    const int4 CN = mr_chunk(a, 1 + (more ? un : u) / tiles);
+    const int4 CN = mine[more ? k + 1 : k];
     MrUnit N = U;
     const float* srcN[MR_J] = {src[0], src[1]};
     const uint8_t *Gn = G, *Pn = P;
@@ -382,6 +396,7 @@ __global__ __launch_bounds__(MR_THREADS) void moe_gate_up_mf(MoeGroupedArgs a) {
     }
     if (!more) break;
     u = un;
+    ++k;
     U = N;
     src[0] = srcN[0];
     src[1] = srcN[1];
@@ -559,10 +574,15 @@ static int mr_grid(const MoeGroupedArgs& a, int tiles, const void* kernel, int t
 // column step and the images fit at once (moe_down_mf).
 static bool mr_halves(int nsb) { return nsb >= 3 && nsb <= MR_GC; }
 
+// The gate/up launch: also enough workgroups that none takes more than
+// MR_UNITS_MAX units.
 template <int KIND>
 static void launch_gate_up_mf(const MoeGroupedArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(moe_gate_up_mf<KIND>, dim3(mr_grid(a, a.I / 64, (const void*)moe_gate_up_mf<KIND>, MR_THREADS)),
-                     dim3(MR_THREADS), 0, s, a);
+  const int tiles = a.I / 64;
+  const long bound = (long)tiles * moe_max_chunks(a.T, a.top_k, std::min(a.n_exp, a.T * a.top_k), MR_J);
+  const int grid = (int)std::max<long>(mr_grid(a, tiles, (const void*)moe_gate_up_mf<KIND>, MR_THREADS),
+                                       (bound + MR_UNITS_MAX - 1) / MR_UNITS_MAX);
+  hipLaunchKernelGGL(moe_gate_up_mf<KIND>, dim3(grid), dim3(MR_THREADS), 0, s, a);
 }
 
 template <int KIND>
@@ -580,7 +600,6 @@ bool moe_mfma_kind(int kind) { return kind == Q4_K || kind == Q6_K; }
 
 template <int GK, int DK>
 static hipError_t launch_mr(const MoeGroupedArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(moe_plan_mf, dim3(1), dim3(1024), 0, s, a);
   launch_gate_up_mf<GK>(a, s);
   launch_down_mf<DK>(a, s);
   hipLaunchKernelGGL(moe_combine_mf, dim3((a.dim + 255) / 256, a.T), dim3(256), 0, s, a);
