@@ -27,9 +27,17 @@ CFLAGS = [
 ]
 
 
+# Per-source flags.  kq_mv_mfma.hip (the batch-1 matrix-core kernels): MFMA
+# results in VGPRs rather than AGPRs, which drops a v_accvgpr_read per result
+# from the 64-row column loops (Q2_K / Q3_K / Q5_K launches of 28672x4096 and
+# up 2-7% faster, the 8B decode +0.2%); the small-batch sources measured equal
+# or slower with it (Q4_K 4096^2 at 64 vectors +12%), so only this file.
+EXTRA_FLAGS = {"kq_mv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src):
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the device feature flag; drop that note.
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
