@@ -296,6 +296,9 @@ PACKED_CASES = [
     # matrix-core down with two halves per 16-row block (3..8 columns of inter)
     (512, 2048, 16, 4, aa.Q4_K, aa.Q6_K, True, 24),     # 8 columns: two steps per half
     (512, 1280, 16, 4, aa.Q6_K, aa.Q4_K, False, 12),    # 5 columns: half 0's second step has one
+    # 64 row tiles of I and 95 tokens: the gate/up unit bound (64 x 557) needs a grid past the resident
+    # workgroups, so that none takes more than the 32 units whose chunks it keeps
+    (256, 4096, 128, 8, aa.Q4_K, aa.Q6_K, True, 95),
     # Q4_K / Q6_K from 96 tokens: the grouped prefill products (kq_moe_prefill.hip)
     (2048, 768, 128, 8, aa.Q4_K, aa.Q6_K, True, 96),    # 16-job groups
     (1024, 512, 16, 2, aa.Q4_K, aa.Q6_K, True, 150),    # 16-job groups, ~19 jobs per expert
