@@ -22,9 +22,9 @@
 // built once per workgroup in LDS and shared by the four waves.  A wave
 // keeps two columns of weights in registers: the next column's loads -- at
 // a unit's last column, the next unit's first and its activations -- are in
-// flight while the current one is multiplied.  A one-job chunk runs the two-job
-// arithmetic with its job repeated and drops the copy.  Every sum is in a
-// fixed order, so the results are deterministic.
+// flight while the current one is multiplied.  A one-job chunk repeats its job
+// in the second slot (every load stays in bounds) and runs the one-job dots.
+// Every sum is in a fixed order, so the results are deterministic.
 #include <math.h>
 
 #include <algorithm>
