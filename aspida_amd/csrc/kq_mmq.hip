@@ -317,15 +317,20 @@ static int mm_rb(int kind, int out_dim, int bp) {
   return kind == Q4_K && bp == 64 && ntiles >= 128 && ntiles % 2 == 0 ? 2 : 1;
 }
 
-// Super-block columns per workgroup: the divisor of nsb whose workgroup count
-// (row groups x column groups) is closest to 4 per CU, with at most 256 / Bpad
-// column groups per row group.
+// Super-block columns per workgroup: the divisor of nsb whose (64-row tile,
+// column group) count is closest to 2 per CU, with at most 256 / Bpad column
+// groups per tile.  Measured on MI355X (Q4_K, cold weights, every split):
+// 14336x4096 at 64 vectors 42 us with two column groups against 46 us with
+// the four a target of 4 workgroups per CU picked, 28672x4096 69 against 80 us
+// with one, 14336x4096 at 32 vectors 26 against 28 us; 4096^2, 8192x4096 and
+// 4096x14336 already sat at their best splits.
 static int mm_spw(int in_dim, int out_dim, int bp, int rb) {
   static const int cus = mm_cus();
-  const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64 / rb;
+  (void)rb;  // a workgroup of two row tiles counts as two
+  const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   const int oks = packed_plan_override_ks();
   if (oks > 0 && nsb % oks == 0 && oks <= 256 / bp) return nsb / oks;
-  const double target = 4.0 * cus;
+  const double target = 2.0 * cus;
   int best_spw = nsb;
   double best = 1e30;
   for (int spw = 1; spw <= nsb; ++spw) {
