@@ -116,6 +116,20 @@ __device__ __forceinline__ void mv16_epilogue(float r, int blk, int out_rows, fl
   if (lane < 16 && row < out_rows) y[row] = r;
 }
 
+// The 16-row block a workgroup takes.  Workgroups go to the 8 XCDs round
+// robin (workgroup p to XCD p % 8), each XCD with its own L2, and the four
+// 16-row blocks of a 64-row tile share the 128-byte lines of the packed
+// group's narrow tail planes (Q2_K's 4-byte, Q3_K's 12- and 2-byte, Q6_K's
+// 2-byte planes: a quarter or half line per block).  So each whole round of
+// 32 workgroups takes 8 tiles, a tile's four blocks on one XCD: p takes tile
+// 8 (p / 32) + p % 8, block (p / 8) % 4.  A last partial round keeps p.  A
+// permutation of [0, n) whatever the dispatch order (which only decides the
+// cache sharing).
+__device__ __forceinline__ int mv16_block(int p, int n) {
+  const int full = n & ~31;
+  return p < full ? (((p >> 5) << 3) + (p & 7)) * 4 + ((p >> 3) & 3) : p;
+}
+
 // Six waves per SIMD for the Q6_K 16-row kernels of 8 or more waves walking
 // their columns one after another (the output head's plan: three 8-wave
 // workgroups per CU), which the registers of the dominant-activation path
@@ -130,7 +144,7 @@ void kq_mv_mfma16(const uint8_t* __restrict__ P, int nsb, int out_rows, const fl
   __shared__ MvShared16 sh[NW];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = blockIdx.x;
+  const int blk = mv16_block(blockIdx.x, gridDim.x);
   const float r = mv_mfma_rows<KIND, PIPE, 1>(P, nsb, blk >> 2, w * spw, spw, x, sh[w].img, sh[w].xsum,
                                               (MvHdr<KIND>*)nullptr, lane, blk & 3);
   mv16_epilogue<NW>(r, blk, out_rows, y);
@@ -154,7 +168,7 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma16_norm(const uint8_t* __re
   __shared__ float part[4];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = blockIdx.x, dim = nsb * 256, n4 = dim / 4;
+  const int blk = mv16_block(blockIdx.x, gridDim.x), dim = nsb * 256, n4 = dim / 4;
   const float4* h4 = reinterpret_cast<const float4*>(H);
   const float4* r4 = reinterpret_cast<const float4*>(r);
   if (threadIdx.x < 256) {
@@ -199,7 +213,7 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma2_16(const uint8_t* __restr
   __shared__ MvShared16 sh[NW];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = blockIdx.x;
+  const int blk = mv16_block(blockIdx.x, gridDim.x);
   if (blk < blocks_a) {
     const float r = mv_mfma_rows<KA, PIPE, 1>(Pa, nsb, blk >> 2, w * spw, spw, x, sh[w].img, sh[w].xsum,
                                               (MvHdr<KA>*)nullptr, lane, blk & 3);
@@ -224,7 +238,7 @@ __global__ __launch_bounds__(64 * NW) void kq_mv_mfma16n(const uint8_t* __restri
   __shared__ float red16[NW][NV][16];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = blockIdx.x;
+  const int blk = mv16_block(blockIdx.x, gridDim.x);
   float r[NV];
   mv_mfma_rows_nv<KIND, 1, NV>(P, nsb, blk >> 2, w * spw, spw, x, (size_t)nsb * 256, nv, sh[w].img, sh[w].xsum,
                                (MvHdr<KIND>*)nullptr, lane, blk & 3, r);

@@ -290,6 +290,22 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   // against 36.8); with rows of up to 16 blocks a column per wave stays
   // better (q|k+v 6144x4096: 6.0 against 6.3).
   const int nsb = in_dim / 256;
+  // Q2_K and Q3_K (more unpacking per byte) on 16-row blocks whose waves
+  // prefetch their next column (two register sets: 95 and 124 VGPRs, no
+  // spill): with rows of up to 64 blocks and one block per CU, or with 1.5 to
+  // 2 blocks per CU.  Measured on MI355X against the 64-row plans below:
+  // Q2_K 4096x14336 7.7 us against 8.8, 8192x8192 7.9 against 8.7,
+  // 8192x14336 12.0 against 12.7; Q3_K 4096x14336 9.8 against 10.3,
+  // 8192x8192 10.1 against 10.4; and against 16 one-column waves (which leave
+  // one Q3_K workgroup per CU at 65 VGPRs) Q3_K 8192x4096 6.2 against 7.4,
+  // 6144x4096 6.1 against 6.8.  Not at 1.25 blocks per CU (Q2_K 5120x14336
+  // slower than 64-row workgroups at 9.9 us).
+  if ((kind == Q2_K || kind == Q3_K) && nsb <= 64 && 4L * ntiles <= 2L * cus &&
+      (2 * 4L * ntiles >= 3L * cus || (nsb > 16 && 4L * ntiles == cus))) {
+    PackedPlan p = mfma16_plan(nsb, 4L * ntiles > cus ? 8 : 16);
+    p.seq = false;
+    return p;
+  }
   if (4L * ntiles <= 2L * cus &&
       (nsb <= 16 || (4L * ntiles >= cus && kind != Q2_K && (kind != Q3_K || nsb <= 32))))
     return mfma16_plan(nsb, 4L * ntiles > cus && nsb > 16 ? 8 : 16);
@@ -303,10 +319,40 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
 }
 
 static PackedPlan mfma64_plan(int kind, int in_dim, int out_dim) {
-  (void)kind;
   static const int cus = device_cus();
   const int nsb = in_dim / 256, ntiles = (out_dim + 63) / 64;
   PackedPlan p{1, 1, nsb};
+  // Q2_K and Q3_K, measured on MI355X against the general choices below:
+  //   * a tile per CU or more, rows of 32+ blocks: Q2_K 4 waves prefetching
+  //     their next column (28672x8192: 19.6 us against 21.2; 57344x8192: 33.7
+  //     against 34.6);
+  //   * 1 to 4 tiles per CU: Q3_K a column per wave, 4 waves per workgroup,
+  //     the row split over nsb/4 workgroups (57344x4096: 24.7 us against 25.9;
+  //     57344x8192: 44.5 against 46.9), but not on more tiles (128256x4096:
+  //     54 against 50);
+  //   * fewer tiles than CUs but two or more groups of 4 per CU, rows of 64+
+  //     blocks: Q2_K 4 groups per tile of 4 waves prefetching nsb/16 columns
+  //     each (8192x28672: 19.5-19.9 us against 21.7-22.2 on one-column waves;
+  //     Q3_K measured 27.1 against 28.5 on one box, 27.2 against 26.3 on
+  //     another, so it keeps one-column waves).
+  if (kind == Q2_K && ntiles >= cus && nsb >= 32 && nsb % 4 == 0) {
+    p.ks = 1;
+    p.nw = 4;
+    p.spw = nsb / 4;
+    return p;
+  }
+  if (kind == Q3_K && ntiles >= cus && ntiles < 4 * cus && nsb % 4 == 0) {
+    p.spw = 1;
+    p.nw = 4;
+    p.ks = nsb / 4;
+    return p;
+  }
+  if (kind == Q2_K && ntiles < cus && 2 * ntiles >= cus && nsb > 64 && nsb % 16 == 0) {
+    p.ks = 4;
+    p.nw = 4;
+    p.spw = nsb / 16;
+    return p;
+  }
   if (ntiles >= cus) {
     p.ks = 1;
     p.nw = pow2_divisor_upto(nsb, 4);

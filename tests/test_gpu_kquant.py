@@ -524,6 +524,30 @@ def test_tall_plans_take_8_wave_16_row_groups(kind, out_dim, in_dim, spw, dev):
     _check_dev(dev, kind, out_dim, in_dim, 6161, "packed", f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} plan={plan}")
 
 
+Q2Q3_PLAN_CASES = [
+    # kind, out, in, (mfma, waves, groups per tile, columns per wave, one after another, 16-row)
+    (aa.Q3_K, 6144, 4096, (True, 8, 1, 2, False, True)),
+    (aa.Q2_K, 4096, 14336, (True, 14, 1, 4, False, True)),
+    (aa.Q2_K, 16448, 8192, (True, 4, 1, 8, False, False)),
+    (aa.Q3_K, 16448, 4096, (True, 4, 4, 1, False, False)),
+    (aa.Q2_K, 8192, 20480, (True, 4, 4, 5, False, False)),
+]
+
+
+@pytest.mark.parametrize("kind,out_dim,in_dim,plan", Q2Q3_PLAN_CASES,
+                         ids=["q3k-two-blocks-per-cu", "q2k-long-rows-block-per-cu", "q2k-tall",
+                              "q3k-tall-split", "q2k-long-rows"])
+def test_q2_q3_plans(kind, out_dim, in_dim, plan, dev):
+    """The Q2_K / Q3_K splits of the MFMA matvec: 16-row workgroups of
+    prefetching waves at 1.5-2 blocks per CU (or one, with long rows), 4
+    prefetching waves per 64-row tile for tall Q2_K, a row split into 4-block
+    groups for tall Q3_K, and 4 groups of 4 waves walking columns for long
+    Q2_K rows -- each the chosen plan, and each matching the oracle."""
+    got = dev.matvec_plan(kind, in_dim, out_dim)
+    assert got == plan, got
+    _check_dev(dev, kind, out_dim, in_dim, 6262 + kind, "packed", f"{aa.KIND_NAMES[kind]} {out_dim}x{in_dim} plan={got}")
+
+
 def test_q8_0_sixteen_wave_column_walk(dev):
     """Q8_0 on 16-wave workgroups walking several columns per wave (more than
     255 tiles, rows of 32 super-blocks) takes the walk without prefetching --

@@ -27,11 +27,19 @@ PLANS = [
     (aa.Q6_K, 8192, 128256, (True, 8, 1, 4, True, True)),     # head: rows of 32 blocks, 16-row
     # K-quant table (Llama-3-8B FFN shapes)
     (aa.Q2_K, 4096, 14336, (True, 16, 1, 1, False, False)),   # a tile per workgroup, a column per wave
-    (aa.Q2_K, 14336, 4096, (True, 8, 7, 1, False, False)),    # long rows stay on 64-row: 8.6 us vs 9.1
+    (aa.Q2_K, 14336, 4096, (True, 14, 1, 4, False, True)),    # 16-row prefetching waves: 7.7 us vs 8.8 on 64-row
     (aa.Q3_K, 4096, 14336, (True, 16, 1, 1, False, False)),
-    (aa.Q3_K, 14336, 4096, (True, 8, 7, 1, False, False)),    # long Q3_K rows on 64-row: 10.6 us vs 11.0
+    (aa.Q3_K, 14336, 4096, (True, 14, 1, 4, False, True)),    # 16-row prefetching waves: 9.8 us vs 10.3
     (aa.Q5_K, 4096, 14336, (True, 16, 1, 1, False, False)),
     (aa.Q5_K, 14336, 4096, (True, 14, 1, 4, True, True)),
+    # Q2_K / Q3_K elsewhere (size sweep, 70B shapes)
+    (aa.Q3_K, 4096, 8192, (True, 8, 1, 2, False, True)),      # 2 blocks per CU, 8 prefetching waves: 6.2 us vs 7.4
+    (aa.Q2_K, 8192, 8192, (True, 8, 1, 4, False, True)),      # 7.9 us vs 8.7 on 64-row
+    (aa.Q2_K, 8192, 57344, (True, 4, 1, 8, False, False)),    # tall: 4 prefetching waves, 33.7 us vs 34.6
+    (aa.Q3_K, 8192, 57344, (True, 4, 8, 1, False, False)),    # tall: rows over 8 groups, 44.5 us vs 46.9
+    (aa.Q3_K, 4096, 128256, (True, 4, 1, 4, True, False)),    # more than 4 tiles per CU: whole tiles
+    (aa.Q2_K, 28672, 8192, (True, 4, 4, 7, False, False)),    # long rows: 19.5 us vs 22.2
+    (aa.Q3_K, 28672, 8192, (True, 8, 14, 1, False, False)),   # long Q3_K rows keep one-column waves
 ]
 
 
