@@ -370,8 +370,8 @@ __device__ __forceinline__ void mmv_dot(const MmvW<Q6_K>& W, const MmvX<Q6_K>& A
   for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(d * __builtin_fmaf(tl[i], 1.f / 2048.f, th[i]), ivs[i], acc[i]);
 }
 
-// Workgroup: RB 16-row blocks (RB = 1: block blockIdx.x, block b % 4 of
-// tile b / 4; RB = 4: tile blockIdx.x) over every column, NW waves each
+// Workgroup: RB 16-row blocks (RB = 1: block b = mv16_block(blockIdx.x),
+// block b % 4 of tile b / 4; RB = 4: tile blockIdx.x) over every column, NW waves each
 // taking columns w spw .. + spw - 1 one after another, NG groups of GV
 // vectors per column (weights loaded once for all of them).  GV = 16 builds
 // the A operands directly in registers; GV = 2 and 4 (batches of up to 4 on
@@ -386,7 +386,8 @@ __global__ __launch_bounds__(64 * NW) void kq_mmv(MmvArgs a) {
   __shared__ MmvStage<GV < 16 ? GV : 1> stage[GV < 16 ? NW : 1];
   const int lane = threadIdx.x & 63, q = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int tile = RB == 4 ? blockIdx.x : blockIdx.x >> 2, rb0 = RB == 4 ? 0 : blockIdx.x & 3;
+  const int b16 = RB == 4 ? 0 : mv16_block(blockIdx.x, gridDim.x);
+  const int tile = RB == 4 ? blockIdx.x : b16 >> 2, rb0 = RB == 4 ? 0 : b16 & 3;
   const int in_dim = a.nsb * 256;
   float acc[RB][NG][4];
 #pragma unroll
