@@ -110,9 +110,10 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0, help="oracle threads (default min(16, cpus))")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--only", choices=["small", "moe", "kquant", "sweep", "decode70", "chain", "prefill", "abi",
-                                       "resident"],
+                                       "resident", "warmcache"],
                     help="run just this table (no decode line): for profiling one workload; 'resident' times "
-                         "the persistent matvec chain experiment beside the decode")
+                         "the persistent matvec chain experiment beside the decode; 'warmcache' times the "
+                         "decode's layer launches with their weights already in the Infinity Cache")
     ap.add_argument("--mv-engine", type=int, choices=[0, 1], default=0,
                     help="batch-1 engine: 0 = MFMA for Q4_K and Q6_K (default), 1 = the VALU kernel for every kind")
     ap.add_argument("--mm-engine", type=int, choices=[0, 1, 2, 3, 4, 5, 6], default=0,
@@ -904,6 +905,41 @@ def copy_probe(torch, mib):
     del a, b
 
 
+def warm_cache_bound(torch, dec, stream, timed, tok_s, steps, warmup):
+    """Experiment, not the headline: what the token would cost if every
+    layer launch found its weights already in the caches.  The 32 layers'
+    launches are issued over layer 0's weights (about 150 MB, inside the
+    256 MB Infinity Cache, so after the first pass each launch reads cache),
+    the head over its own (cold: 431 MB), in one graph timed as the decode
+    is.  The gap to the cold token bounds what any scheme that fetches the
+    next launch's weights ahead of it could gain."""
+    ops = list(dec.launches())
+    per_layer = len(LAYER_LAUNCHES)
+    layer0, head = ops[:per_layer], ops[-1]
+    nlayers = (len(ops) - 1) // per_layer
+
+    def run(op_list):
+        def fn(sp):
+            for op in op_list:
+                dec.issue(op, sp)
+        wall, _ = timed(fn, steps, warmup)
+        return wall / steps
+
+    cold = run(ops)
+    warm = run(layer0 * nlayers + [head])
+    per_launch = {}
+    for i, names in enumerate(LAYER_LAUNCHES):
+        own = [ops[l * per_layer + i] for l in range(nlayers)]   # the 32 layers' copies of this launch
+        per_launch["|".join(names)] = {"cold_us": round(run(own) * 1e6 / nlayers, 2),
+                                       "warm_us": round(run([own[0]] * nlayers) * 1e6 / nlayers, 2)}
+    return {"decode_tok_s": round(tok_s, 2), "token_cold_us": round(cold * 1e6, 1),
+            "token_layers_warm_us": round(warm * 1e6, 1), "tok_s_cold": round(1 / cold, 1),
+            "tok_s_layers_warm": round(1 / warm, 1), "per_launch": per_launch,
+            "note": "the token's launches with the layers over layer 0's weights (cache-resident) against the "
+                    "32 layers' own (HBM); the head is cold in both. per_launch: one launch kind, 32 in a graph, "
+                    "over the 32 layers' weights (cold) or layer 0's (warm)"}
+
+
 def timed_graph(torch, stream, step_fn, steps, warmup):
     """Capture one token, replay `warmup` times, then time `steps` replays
     (wall clock around synchronised replays, and HIP events on the stream)."""
@@ -971,7 +1007,7 @@ def main():
         print(json.dumps({"decode_70b": decode_70b(torch, aa, synth, args.seed, stream, args.mv_engine, args.steps,
                                                    args.warmup)}), flush=True)
         return
-    if args.only and args.only != "resident":
+    if args.only and args.only not in ("resident", "warmcache"):
         if args.copy_probe_mib:
             copy_probe(torch, args.copy_probe_mib)
         if args.only == "abi":
@@ -1002,6 +1038,10 @@ def main():
     tok_s = args.steps / wall
     print(f"# decode (per-matrix launches): {args.steps} tokens in {wall * 1e3:.1f} ms wall "
           f"({gpu_s * 1e3:.1f} ms events) = {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
+    if args.only == "warmcache":
+        print(json.dumps({"warm_cache": warm_cache_bound(torch, dec, stream, timed, tok_s, args.steps,
+                                                         args.warmup)}), flush=True)
+        return
     if args.only == "resident":
         # Experiment, not the headline: the same token as one persistent
         # resident-chain launch (aspida_kq_chain_*), measured slower than the
