@@ -685,20 +685,6 @@ struct MvShared16 {
 // How a wave walks its columns: one column; two register sets in turn (the
 // next column's loads in flight during this one's work); one register set,
 // columns one after another (fewer registers, so more waves per CU).
-// The 16-row block a workgroup takes.  Workgroups go to the 8 XCDs round
-// robin (workgroup p to XCD p % 8), each XCD with its own L2, and the four
-// 16-row blocks of a 64-row tile share the 128-byte lines of the packed
-// group's narrow tail planes (Q2_K's 4-byte, Q3_K's 12- and 2-byte, Q6_K's
-// 2-byte planes: a quarter or half line per block).  So each whole round of
-// 32 workgroups takes 8 tiles, a tile's four blocks on one XCD: p takes tile
-// 8 (p / 32) + p % 8, block (p / 8) % 4.  A last partial round keeps p.  A
-// permutation of [0, n) whatever the dispatch order (which only decides the
-// cache sharing).
-__device__ __forceinline__ int mv16_block(int p, int n) {
-  const int full = n & ~31;
-  return p < full ? (((p >> 5) << 3) + (p & 7)) * 4 + ((p >> 3) & 3) : p;
-}
-
 constexpr int MV_ONE = 0, MV_PF = 1, MV_SEQ = 2;
 
 //

@@ -52,6 +52,20 @@ __host__ __device__ constexpr int packed_offset(int kind, int r, int b) {
   }
 }
 
+// The 16-row block a workgroup takes.  Workgroups go to the 8 XCDs round
+// robin (workgroup p to XCD p % 8), each XCD with its own L2, and the four
+// 16-row blocks of a 64-row tile share the 128-byte lines of the packed
+// group's narrow tail planes (Q2_K's 4-byte, Q3_K's 12- and 2-byte, Q6_K's
+// 2-byte planes: a quarter or half line per block).  So each whole round of
+// 32 workgroups takes 8 tiles, a tile's four blocks on one XCD: p takes tile
+// 8 (p / 32) + p % 8, block (p / 8) % 4.  A last partial round keeps p.  A
+// permutation of [0, n) whatever the dispatch order (which only decides the
+// cache sharing).
+__host__ __device__ constexpr int mv16_block(int p, int n) {
+  const int full = n & ~31;
+  return p < full ? (((p >> 5) << 3) + (p & 7)) * 4 + ((p >> 3) & 3) : p;
+}
+
 // Whole-chunk loads of row `lane`'s super-block from the group at g;
 // non-temporal (NT) when the launch reads the group once.
 template <int C, bool NT = true>

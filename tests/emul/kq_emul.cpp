@@ -64,6 +64,9 @@ extern "C" void kq_emul_ld12e(const uint8_t* p, uint8_t* out) {
 // its 64-row group.
 extern "C" int kq_emul_packed_offset(int kind, int r, int b) { return kq::packed_offset(kind, r, b); }
 
+// The 16-row block physical workgroup p of n takes (kq_packed.h).
+extern "C" int kq_emul_mv16_block(int p, int n) { return kq::mv16_block(p, n); }
+
 // Row `lane`'s dot over one super-block column of a packed 64-row group, as
 // kq_mv_packed forms it: the lane's registers from Packed<K>::load, the four
 // quarters from Packed<K>::quarter, activations xs and per-16 sums s16.

@@ -105,3 +105,24 @@ def test_packed_rows_match_oracle(emul, kind):
                     for r in range(64)])
     err = np.abs(got - ref) / np.maximum(scale, 1e-30)
     assert err.max() < 1e-6, err.max()
+
+
+def test_mv16_block_order_is_a_permutation_keeping_tiles_on_one_xcd(emul):
+    """The 16-row kernels' block order (mv16_block, kq_packed.h): for every
+    grid size it is a permutation of the blocks, so each block is computed
+    exactly once; within whole rounds of 32 workgroups the four blocks of a
+    64-row tile go to workgroups of one XCD (workgroup p on XCD p % 8) and of
+    one round, and the rows of a partial last round keep their order."""
+    f = emul.kq_emul_mv16_block
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_int, ctypes.c_int]
+    for n in list(range(1, 300)) + [1000, 1024, 4096, 8017, 32064]:
+        blocks = [f(p, n) for p in range(n)]
+        assert sorted(blocks) == list(range(n)), n
+        full = n - n % 32
+        where = {b: p for p, b in enumerate(blocks)}
+        for t in range(full // 4):
+            ps = [where[4 * t + r] for r in range(4)]
+            assert len({p % 8 for p in ps}) == 1, (n, t, ps)
+            assert len({p // 32 for p in ps}) == 1, (n, t, ps)
+        assert blocks[full:] == list(range(full, n)), n
