@@ -281,9 +281,11 @@ static PackedPlan mfma_plan_choice(int kind, int in_dim, int out_dim) {
   // every CU (otherwise few CUs would walk long column runs).  Measured on
   // MI355X: Q4_K 4096x4096 4.3 us against 5.8 us on 64-row workgroups with
   // partial sums; 1024x14336 5.9 us on 64-row workgroups against 8.1 us.
-  // Q2_K streams fewer bytes per column for the same arithmetic, so long
-  // column runs stay on 64-row workgroups (4096x14336: 8.6 us against 9.1);
-  // so do Q3_K rows of more than 32 blocks (8192x28672: 29.4 us against 31.3).
+  // Q2_K streams fewer bytes per column for the same arithmetic, so its long
+  // column runs walked one after another stay on 64-row workgroups
+  // (4096x14336: 8.6 us against 9.1; the prefetching 16-row rule above takes
+  // that shape now); so do Q3_K rows of more than 32 blocks (8192x28672: 29.4
+  // us against 31.3).
   // With more 16-row blocks than CUs, two blocks share a CU: when 16 waves
   // would still walk several columns each, 8 waves keep both resident (Q4_K
   // 8192x8192: 9.2 us against 10.1 with 16 waves; Q6_K 8192x28672: 35.7
