@@ -1073,6 +1073,17 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
                                              const void* up_p, int gu_kind, const void* down_p, int down_kind,
                                              const void* shg_p, const void* shu_p, const void* shd_p,
                                              const float* shared_gate_inp, void* work, float* y, void* stream) {
+  return kq::moe_experts_packed_norm(x, T, dim, top_k, intermed, n_exp, top_idx, top_w, gate_p, up_p, gu_kind, down_p,
+                                     down_kind, shg_p, shu_p, shd_p, shared_gate_inp, work, y, stream, nullptr,
+                                     nullptr, nullptr, nullptr);
+}
+
+int kq::moe_experts_packed_norm(const float* x, int T, int dim, int top_k, int intermed, int n_exp,
+                                const int* top_idx, const float* top_w, const void* gate_p, const void* up_p,
+                                int gu_kind, const void* down_p, int down_kind, const void* shg_p, const void* shu_p,
+                                const void* shd_p, const float* shared_gate_inp, void* work, float* y, void* stream,
+                                float* norm_h, const float* norm_w, float* norm_nx, bool* norm_done) {
+  if (norm_done) *norm_done = false;
   const bool ok = x && top_idx && top_w && gate_p && up_p && down_p && shg_p && shu_p && shd_p && work && y &&
                   valid_kind(gu_kind) && valid_kind(down_kind) && T > 0 && n_exp > 0 && top_k > 0 &&
                   top_k <= n_exp && kq::moe_grouped_supported(dim, intermed, 1, top_k) &&
@@ -1116,9 +1127,18 @@ extern "C" int aspida_moe_experts_packed_dev(const float* x, int T, int dim, int
     a.top_w = top_w + (size_t)t0 * top_k;
     a.y = y + (size_t)t0 * dim;
     kq::moe_grouped_bind(a, work);
+    // The norm goes into the combine only when every chunk's launch takes it.
+    bool done = false;
+    if (norm_h && norm_w && norm_nx && chunk >= T) {
+      a.norm_h = norm_h + (size_t)t0 * dim;
+      a.norm_w = norm_w;
+      a.norm_nx = norm_nx + (size_t)t0 * dim;
+      a.norm_done = &done;
+    }
     const int rc = check(kq::launch_moe_grouped(a, gu_kind, down_kind, (hipStream_t)stream),
                          "aspida_moe_experts_packed_dev");
     if (rc) return rc;
+    if (norm_done) *norm_done = done;
   }
   return 0;
 }

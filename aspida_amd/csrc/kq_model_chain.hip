@@ -307,10 +307,16 @@ int norm_route(Chain& c, const Layer& L, int B, const float* pend, const float* 
   return ep(aspida_moe_route_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.nx, c.rl, c.idx, c.tw, c.st), "chain router");
 }
 
-int moe_apply(Chain& c, const Layer& L, int B) {
+// The experts of one layer into c.y.  With next_norm set, the combine launch
+// (when the experts' path has one) also adds c.y into H and forms
+// nx = RMSNorm(H) with those weights -- the step's next add_norm -- and
+// *normed says whether it did.
+int moe_apply(Chain& c, const Layer& L, int B, const float* next_norm = nullptr, bool* normed = nullptr) {
+  if (normed) *normed = false;
   if (L.grouped)
-    return ep(aspida_moe_experts_packed_dev(c.nx, B, c.dim, L.top_k, L.intermed, L.n_exp, c.idx, c.tw, L.g, L.u, L.gk,
-                                            L.dn, L.dk, L.sg, L.su, L.sd, L.sgi, c.work, c.y, c.st),
+    return ep(kq::moe_experts_packed_norm(c.nx, B, c.dim, L.top_k, L.intermed, L.n_exp, c.idx, c.tw, L.g, L.u, L.gk,
+                                          L.dn, L.dk, L.sg, L.su, L.sd, L.sgi, c.work, c.y, c.st,
+                                          next_norm ? c.H : nullptr, next_norm, next_norm ? c.nx : nullptr, normed),
               "chain experts");
   return ep(aspida_moe_experts_dev(c.nx, B, c.dim, L.top_k, L.intermed, L.n_exp, c.idx, c.tw, L.g, L.g_stride, L.gk,
                                    L.u, L.u_stride, L.uk, L.dn, L.d_stride, L.dk, L.sg, L.sgk, L.su, L.suk, L.sd, L.sdk,
@@ -326,6 +332,14 @@ int record(Chain& c, int B, int n_layers, bool logits) {
                      c.st, c.embed, c.rows, c.dim, c.H);
   if (int rc = hip(hipGetLastError(), "chain embed")) return rc;
   const float* pend = nullptr;  // the residual still to be added to H
+  bool normed = false;          // H holds its residual and nx its next norm already (the experts' combine)
+  // The norm that follows layer l's experts: the next layer's attention norm
+  // (or its post-attention norm when it has no mixer), else the final norm.
+  const auto next_norm = [&](int l) -> const float* {
+    if (l + 1 >= n_layers) return c.fnorm;
+    const Layer& N = c.layers[l + 1];
+    return N.has_mix ? N.attn_norm : N.has_moe ? N.post_norm : nullptr;
+  };
   for (int l = 0; l < n_layers; ++l) {
     const Layer& L = c.layers[l];
     if (L.has_mix && B == 1 && L.has_moe && L.mix.kind >= 0 &&
@@ -342,17 +356,29 @@ int record(Chain& c, int B, int n_layers, bool logits) {
       if (rc != -ENOTSUP) return ep(rc, "chain mixer with norm");
     }
     if (L.has_mix) {
-      if (int rc = add_norm(c, B, pend, L.attn_norm)) return rc;
+      if (!normed)
+        if (int rc = add_norm(c, B, pend, L.attn_norm)) return rc;
+      normed = false;
       if (int rc = mat_apply(c, L.mix, B, c.nx, c.ao)) return rc;
       pend = c.ao;
     }
     if (L.has_moe) {
-      if (int rc = norm_route(c, L, B, pend, nullptr)) return rc;
-      if (int rc = moe_apply(c, L, B)) return rc;
-      pend = c.y;
+      if (normed) {
+        if (int rc = ep(aspida_moe_route_dev(L.router, L.n_exp, c.dim, B, L.top_k, c.nx, c.rl, c.idx, c.tw, c.st),
+                        "chain router"))
+          return rc;
+      } else if (int rc = norm_route(c, L, B, pend, nullptr)) {
+        return rc;
+      }
+      // From 2 lanes the experts' combine is a launch of its own, which then
+      // also takes the next add_norm.
+      const float* nn = B > 1 ? next_norm(l) : nullptr;
+      if (int rc = moe_apply(c, L, B, nn, &normed)) return rc;
+      pend = normed ? nullptr : c.y;
     }
   }
-  if (int rc = add_norm(c, B, pend, c.fnorm)) return rc;
+  if (!normed)
+    if (int rc = add_norm(c, B, pend, c.fnorm)) return rc;
   return logits ? mat_apply(c, c.lm, B, c.nx, c.dlog) : 0;
 }
 

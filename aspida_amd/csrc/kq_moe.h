@@ -73,6 +73,15 @@ struct MoeGroupedArgs {
   int T, top_k, n_exp, dim, I;
   int tiles_dim;         // 64-row tiles of dim (vector-ALU down projection)
   int blocks_dim;        // 16-row blocks of dim (matrix-core down projection)
+  // Optional (a model chain's next norm in the combine launch): when norm_h is
+  // set and the launch path combines in a launch of its own (matrix cores,
+  // T >= 2), that launch also adds y[t] into norm_h[t] and writes
+  // norm_nx[t] = RMSNorm(norm_h[t]) with weights norm_w, and sets the host
+  // flag *norm_done.  Other paths leave the three alone.
+  float* norm_h = nullptr;
+  const float* norm_w = nullptr;
+  float* norm_nx = nullptr;
+  bool* norm_done = nullptr;
 };
 
 size_t moe_grouped_work_bytes(int T, int dim, int I, int top_k);
@@ -88,6 +97,16 @@ bool moe_grouped_experts_ok(int n_exp);
 // other kinds -- and every kind under aspida_kq_set_mv_engine(1) -- on the
 // vector ALUs (64-row tiles).
 hipError_t launch_moe_grouped(const MoeGroupedArgs& a, int gu_kind, int down_kind, hipStream_t s);
+// aspida_moe_experts_packed_dev with the model chain's next norm taken into
+// the combine launch where the path has one (MoeGroupedArgs::norm_h): then
+// y[t] is also added into norm_h[t], norm_nx[t] = RMSNorm(norm_h[t]) with
+// weights norm_w, and *norm_done is set; otherwise *norm_done is false and
+// norm_h, norm_nx are untouched.  Null norm pointers: the plain entry point.
+int moe_experts_packed_norm(const float* x, int T, int dim, int top_k, int intermed, int n_exp, const int* top_idx,
+                            const float* top_w, const void* gate_p, const void* up_p, int gu_kind,
+                            const void* down_p, int down_kind, const void* shg_p, const void* shu_p,
+                            const void* shd_p, const float* shared_gate_inp, void* work, float* y, void* stream,
+                            float* norm_h, const float* norm_w, float* norm_nx, bool* norm_done);
 // The grouped launches on the matrix cores (kq_moe_mfma.hip): Q4_K and Q6_K
 // projections, any T; hipErrorNotSupported for other kinds.
 bool moe_mfma_kind(int kind);

@@ -540,6 +540,90 @@ __global__ __launch_bounds__(256) void moe_combine_mf(MoeGroupedArgs a) {
   if (valid) a.y[(size_t)t * a.dim + row] = acc + gs * vs;
 }
 
+// The combine of token t (blockIdx.x), then H[t] += y[t] and
+// nx[t] = (H[t] / rms) * w with rms = sqrt(mean(H[t]^2) + 1e-6)
+// (LLM_RMSNorm.Forward, src/llm/llm_rmsnorm.adb:10-41): moe_combine_mf's
+// arithmetic per element and the one-workgroup norm of the model chain's
+// chain_add_norm (256 threads, float4 per thread and step, the same order of
+// the sum of squares), so the results are those of the two launches it
+// replaces.  A token with an invalid expert id keeps its y, which is still
+// added, as the two launches would.
+constexpr int MR_NORM_THREADS = 256;
+constexpr int MR_NORM_HELD = 4;  // float4 per thread held in registers: rows of up to 4096
+__global__ __launch_bounds__(MR_NORM_THREADS) void moe_combine_norm_mf(MoeGroupedArgs a) {
+  __shared__ float part[MR_NORM_THREADS / 64];
+  __shared__ float wk[MOE_MAX_TOPK];
+  const int t = blockIdx.x, slots = a.top_k + 1, n4 = a.dim / 4;
+  if ((int)threadIdx.x < a.top_k) wk[threadIdx.x] = a.top_w[t * a.top_k + threadIdx.x];
+  const float gs = a.gsh[t];
+  bool valid = true;
+  for (int k = 0; k < a.top_k; ++k) {
+    const int e = a.idx[t * a.top_k + k];
+    valid = valid && e >= 0 && e < a.n_exp;
+  }
+  __syncthreads();
+  float4* __restrict__ h = reinterpret_cast<float4*>(a.norm_h + (size_t)t * a.dim);
+  float4* __restrict__ y4 = reinterpret_cast<float4*>(a.y + (size_t)t * a.dim);
+  const float4* __restrict__ yt = reinterpret_cast<const float4*>(a.yk + (size_t)t * slots * a.dim);
+  const float4* __restrict__ w4 = reinterpret_cast<const float4*>(a.norm_w);
+  float4* __restrict__ nx = reinterpret_cast<float4*>(a.norm_nx + (size_t)t * a.dim);
+  // y = sum_k top_w[k] yk[k] (ascending k) + g_t yk[top_k], then v = H + y.
+  const auto sum_row = [&](int i) {
+    float4 yv;
+    if (valid) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k = 0; k < a.top_k; ++k) {
+        const float4 v = yt[(size_t)k * n4 + i];
+        const float w = wk[k];
+        acc = make_float4(acc.x + w * v.x, acc.y + w * v.y, acc.z + w * v.z, acc.w + w * v.w);
+      }
+      const float4 vs = yt[(size_t)a.top_k * n4 + i];
+      yv = make_float4(acc.x + gs * vs.x, acc.y + gs * vs.y, acc.z + gs * vs.z, acc.w + gs * vs.w);
+      y4[i] = yv;
+    } else {
+      yv = y4[i];
+    }
+    const float4 hv = h[i];
+    const float4 v = make_float4(hv.x + yv.x, hv.y + yv.y, hv.z + yv.z, hv.w + yv.w);
+    h[i] = v;
+    return v;
+  };
+  float ss = 0.f;
+  const auto square = [&](const float4& v) {
+    ss += v.x * v.x;
+    ss += v.y * v.y;
+    ss += v.z * v.z;
+    ss += v.w * v.w;
+  };
+  float4 held[MR_NORM_HELD];
+#pragma unroll
+  for (int q = 0; q < MR_NORM_HELD; ++q) {
+    const int i = (int)threadIdx.x + q * MR_NORM_THREADS;
+    if (i < n4) {
+      held[q] = sum_row(i);
+      square(held[q]);
+    }
+  }
+  for (int i = (int)threadIdx.x + MR_NORM_HELD * MR_NORM_THREADS; i < n4; i += MR_NORM_THREADS) square(sum_row(i));
+  ss = wave_total(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < MR_NORM_THREADS / 64; ++k) tot += part[k];
+  const float rms = sqrtf(tot / (float)a.dim + 1e-6f);
+  const auto norm = [&](int i, const float4& v) {
+    const float4 g = w4[i];
+    nx[i] = make_float4((v.x / rms) * g.x, (v.y / rms) * g.y, (v.z / rms) * g.z, (v.w / rms) * g.w);
+  };
+#pragma unroll
+  for (int q = 0; q < MR_NORM_HELD; ++q) {
+    const int i = (int)threadIdx.x + q * MR_NORM_THREADS;
+    if (i < n4) norm(i, held[q]);
+  }
+  for (int i = (int)threadIdx.x + MR_NORM_HELD * MR_NORM_THREADS; i < n4; i += MR_NORM_THREADS) norm(i, h[i]);
+}
+
 // ---- launchers ------------------------------------------------------------------
 
 // Resident workgroups of a kernel on the current device (per CU times CUs),
@@ -602,7 +686,12 @@ template <int GK, int DK>
 static hipError_t launch_mr(const MoeGroupedArgs& a, hipStream_t s) {
   launch_gate_up_mf<GK>(a, s);
   launch_down_mf<DK>(a, s);
-  hipLaunchKernelGGL(moe_combine_mf, dim3((a.dim + 255) / 256, a.T), dim3(256), 0, s, a);
+  if (a.norm_h && a.norm_w && a.norm_nx && a.dim % 4 == 0) {
+    hipLaunchKernelGGL(moe_combine_norm_mf, dim3(a.T), dim3(MR_NORM_THREADS), 0, s, a);
+    if (a.norm_done) *a.norm_done = true;
+  } else {
+    hipLaunchKernelGGL(moe_combine_mf, dim3((a.dim + 255) / 256, a.T), dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

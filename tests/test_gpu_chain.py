@@ -289,6 +289,44 @@ def test_model_chain_batch_lanes():
         ch.reset()
 
 
+# Layers whose experts' combine takes the next norm at two lanes and more: a
+# grouped matrix-core layer followed by one without a mixer (the combine forms
+# the post-attention norm and the router reads it), that one followed by a
+# mixer layer (the attention norm), and a last layer (the final norm).
+FUSED_NORM_LAYERS = [
+    (Q4, -1, (Q4, Q4, Q6, Q4, Q4, Q6), True),
+    (None, -1, (Q4, Q4, Q6, Q4, Q4, Q6), True),
+    (-1, Q4, (Q4, Q4, Q6, Q4, Q4, Q6), False),
+]
+
+
+def test_model_chain_norm_in_expert_combine():
+    """Lane batches through layers whose experts' combine launch also adds the
+    residual and forms the next norm: every lane's logits and residual stream
+    against the oracle and against its single-token forward (which keeps the
+    separate norm launches)."""
+    gen = synth.rng(2718)
+    dim, inter, n_exp, top_k = 512, 256, 16, 4
+    M = _chain_model(gen, dim, inter, n_exp, top_k, 500, 64, FUSED_NORM_LAYERS)
+    ch = _register(M)
+    try:
+        for B in (2, 8):
+            rows = gen.integers(0, 64, B).astype(np.int32)
+            got = ch.forward_batch(rows)
+            for b, r in enumerate(rows):
+                _, want, routes = oracle.chain_forward(M, int(r))
+                _no_near_ties(routes, top_k, f"B={B} lane {b}")
+                _close(got[b], want, f"B={B} lane {b} (row {r})")
+                _close(got[b], ch.forward(int(r)).astype(np.float64), f"B={B} lane {b} vs single")
+            for n in (1, 2, 3):
+                H = ch.hidden(rows, n)
+                for b, r in enumerate(rows):
+                    _close(H[b], oracle.chain_forward(M, int(r), n_layers=n, logits=False)[0],
+                           f"B={B} lane {b} hidden after {n} layers")
+    finally:
+        ch.reset()
+
+
 def test_model_chain_graph_replay_matches_eager():
     """The first forward of a lane count runs eagerly and captures a graph; later ones
     replay it.  Replays, with eager work and synchronisation between them, give the
